@@ -1,0 +1,236 @@
+"""Benchmark of the int8 quantised-matmul hot path on one MI355X.
+
+Metric: int8 GEMM TOPS + GEMV HBM GB/s (% of MI355X roofline), 1 GPU.
+
+One step = one pass of the reference operator try_int8_gemm (per-row int8
+quantisation of the f16 activations + W8A8 int8-MFMA GEMM with the fused
+epilogue, f32 out) over the north_star GEMM "4096x3072x12288" in both
+orientations: M=4096,K=3072,N=12288 and M=4096,K=12288,N=3072. ``value`` is
+int8 TOPS = 2*M*N*K / time over the timed steps, inputs resident in HBM.
+
+The weight-only GEMV (M=1, K=4096, N=14336, fp16 scales) is reported beside
+it under "gemv", in HBM GB/s, over a rotation of weight copies larger than the
+256 MB Infinity Cache so that no launch re-reads its weights from that cache.
+
+"roofline" describes the dominant kernel (the W8A8 GEMM), timed alone with
+HIP events on the stream it is launched on; "cpu_baseline" times the CPU
+oracle (a C restatement of the reference's int8_host::gemm, single thread)
+on a bounded sample of the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "omni-rs_amd"))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+PEAK_INT8_TOPS = 5000.0     # MI355X dense int8 MFMA, 5.0 POP/s
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, 8 TB/s
+GEMM_SHAPES = [(4096, 3072, 12288), (4096, 12288, 3072)]  # (M, K, N)
+GEMV_SHAPE = (1, 4096, 14336)
+GEMV_ROTATION_BYTES = 1 << 30
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--cpu-seconds", type=float, default=10.0,
+                   help="bounded CPU-baseline sample length")
+    return p.parse_args()
+
+
+def timed(fn, iters, stream):
+    import torch
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    stop.record(stream)
+    stop.synchronize()
+    return start.elapsed_time(stop) / 1e3  # seconds
+
+
+def load_traffic():
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE and
+    WRITE_SIZE, scaled by a copy-kernel calibration); null if not measured."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return {}
+    with open(path) as f:
+        return json.load(f)
+
+
+def cpu_baseline(oracle, np, seconds):
+    """Reference CPU path (C restatement of int8_host::gemm, 1 thread) on the
+    first rows of the north_star GEMM, growing the sample until `seconds`."""
+    M, K, N = GEMM_SHAPES[0]
+    rng = np.random.default_rng(0)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    scale = rng.uniform(0.002, 0.02, N).astype(np.float32)
+    zero = np.zeros(N, np.int32)
+    rows, elapsed = 0, 0.0
+    while elapsed < seconds and rows < M:
+        x = rng.standard_normal((2, K)).astype(np.float16).astype(np.float32)
+        t0 = time.perf_counter()
+        oracle.int8_gemm(x, w, scale, zero)
+        elapsed += time.perf_counter() - t0
+        rows += 2
+    ops = 2.0 * rows * N * K
+    return {"value": ops / elapsed / 1e12, "unit": "TOPS", "cores": 1, "kind": "port",
+            "sample": f"{rows} rows of M={M},K={K},N={N} (f16 x -> int8 codes, int32 acc, "
+                      f"f32 epilogue), {elapsed:.1f} s single-thread C restatement of "
+                      f"int8_host.rs:19-53"}
+
+
+def cpu_gemv_baseline(oracle, np, seconds):
+    """Reference-style CPU weight-only route (dequantise to f16, f32 dot) on
+    the GEMV shape, columns sampled until `seconds`."""
+    M, K, N = GEMV_SHAPE
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    cols, elapsed = 0, 0.0
+    while elapsed < seconds and cols < N:
+        w = rng.integers(-127, 128, (256, K), dtype=np.int8)
+        s = rng.uniform(0.002, 0.02, 256).astype(np.float16)
+        t0 = time.perf_counter()
+        oracle.w8a16_gemm(x, w, s)
+        elapsed += time.perf_counter() - t0
+        cols += 256
+    return {"value": cols * K / elapsed / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{cols} of {N} output channels at M={M},K={K} (int8 weights streamed), "
+                      f"{elapsed:.1f} s single-thread C restatement"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the path shards by output columns across GPUs, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import omni_int8 as oi
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if not oi.arch_supported(0):
+        raise SystemExit("cuda:0 is not gfx950")
+    stream = torch.cuda.current_stream(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+
+    # ---- W8A8: inputs resident in HBM --------------------------------------
+    cases = []
+    for M, K, N in GEMM_SHAPES:
+        x = torch.randn((M, K), generator=gen, device=dev, dtype=torch.float32).half()
+        w = torch.randint(-127, 128, (N, K), generator=gen, device=dev, dtype=torch.int8)
+        w_packed = w.view(torch.int32).reshape(-1)
+        scale = torch.rand(N, generator=gen, device=dev) * 0.018 + 0.002
+        zero = torch.zeros(N, dtype=torch.int32, device=dev)
+        codes, rs, total = oi.quantize_rows(x)
+        cases.append(dict(M=M, K=K, N=N, x=x, w=w, w_packed=w_packed, scale=scale, zero=zero,
+                          codes=codes, rs=rs, total=total))
+
+    def step():
+        for c in cases:
+            oi.try_int8_gemm(c["x"], c["w_packed"], c["scale"], c["zero"])
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t_steps = timed(step, args.steps, stream)
+    torch.cuda.synchronize()
+    ops_per_step = sum(2.0 * c["M"] * c["N"] * c["K"] for c in cases)
+    tops = ops_per_step * args.steps / t_steps / 1e12
+
+    # dominant kernel alone: the GEMM on pre-quantised codes, per orientation
+    gemm_time = 0.0
+    per_shape = []
+    for c in cases:
+        out = torch.empty((c["M"], c["N"]), dtype=torch.float32, device=dev)
+
+        def one(c=c):
+            oi.w8a8_gemm(c["codes"], c["rs"], c["total"], c["w"], c["scale"], c["zero"])
+
+        for _ in range(5):
+            one()
+        t = timed(one, args.steps, stream) / args.steps
+        gemm_time += t
+        per_shape.append({"M": c["M"], "K": c["K"], "N": c["N"], "gemm_us": round(t * 1e6, 2),
+                          "gemm_tops": round(2.0 * c["M"] * c["N"] * c["K"] / t / 1e12, 1)})
+        del out
+    gemm_tops = ops_per_step / gemm_time / 1e12
+    traffic = load_traffic()
+
+    # ---- W8A16 GEMV over rotating weight copies ---------------------------------
+    gM, gK, gN = GEMV_SHAPE
+    copies = max(4, -(-GEMV_ROTATION_BYTES // (gN * gK)))
+    gx = torch.randn((gM, gK), generator=gen, device=dev).half()
+    gws = [torch.randint(-127, 128, (gN, gK), generator=gen, device=dev, dtype=torch.int8)
+           for _ in range(copies)]
+    gs = (torch.rand(gN, generator=gen, device=dev) * 0.018 + 0.002).half()
+    idx = [0]
+
+    def gemv():
+        oi.w8a16_linear(gx, gws[idx[0] % copies], gs)
+        idx[0] += 1
+
+    for _ in range(2 * copies):
+        gemv()
+    gemv_iters = copies * max(1, args.steps // 4)
+    t_gemv = timed(gemv, gemv_iters, stream) / gemv_iters
+    gemv_bytes = gN * gK + 2 * gN + 2 * gM * gK + 2 * gM * gN
+    gemv_gbs = gemv_bytes / t_gemv / 1e9
+
+    # ---- CPU baselines (oracle, bounded samples) -----------------------------
+    import oracle_lib
+    oracle = oracle_lib.Oracle()
+    cpu = cpu_baseline(oracle, np, args.cpu_seconds)
+    cpu_gemv = cpu_gemv_baseline(oracle, np, max(2.0, args.cpu_seconds / 2))
+
+    line = {
+        "metric": "int8 GEMM TOPS + GEMV HBM GB/s (% of MI355X roofline), 1 GPU",
+        "value": round(tops, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t_steps / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic: x ~ N(0,1) f16, W ~ U[-127,127] int8, scales ~ U[0.002,0.02]",
+        "config": {"workload": "try_int8_gemm (quantize_rows + W8A8 GEMM, f32 out) at "
+                               "M=4096,K=3072,N=12288 and M=4096,K=12288,N=3072",
+                   "gemm_shapes": per_shape},
+        "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 1), "peak": PEAK_INT8_TOPS,
+                     "unit": "TFLOP/s", "ops": "int8 MACs x2 (TOPS)",
+                     "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
+                     "traffic": traffic.get("w8a8_gemm")},
+        "cpu_baseline": cpu,
+        "gemv": {
+            "metric": "W8A16 GEMV HBM GB/s", "value": round(gemv_gbs, 1), "unit": "GB/s",
+            "config": {"M": gM, "K": gK, "N": gN, "weight_copies": copies,
+                       "rotation_bytes": copies * gN * gK},
+            "us_per_launch": round(t_gemv * 1e6, 3),
+            "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(gemv_gbs / PEAK_HBM_GBS, 4),
+                         "traffic": traffic.get("w8a16_gemv")},
+            "cpu_baseline": cpu_gemv,
+        },
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

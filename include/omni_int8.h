@@ -1,0 +1,138 @@
+/*
+ * omni_int8 — MI355X (gfx950) int8 quantised-matmul hot path, C ABI.
+ *
+ * This is the drop-in boundary for omni-rs's int8 matmul operator. Every
+ * entry point takes plain device pointers, sizes and a HIP stream handle
+ * (hipStream_t passed as void*, NULL = the null stream). The library
+ * allocates nothing: the caller owns every buffer, including the workspace
+ * omni_try_int8_gemm needs. Calls are asynchronous on `stream`; calls on
+ * distinct streams may run concurrently.
+ *
+ * Return status (mirrors the reference's Option convention):
+ *   OMNI_OK (0)            the work was enqueued;
+ *   OMNI_NOT_HANDLED (1)   shapes disagree — the reference returns None here
+ *                          and its caller panics or falls back;
+ *   OMNI_NO_DEVICE (2)     the current device is not gfx950;
+ *   OMNI_BAD_ARGUMENT (3)  a null pointer, a negative size, an unknown dtype
+ *                          or a misaligned buffer;
+ *   OMNI_HIP_ERROR (-1)    a HIP launch failed; omni_int8_last_error() says why.
+ *
+ * Data layouts (all row-major, no padding):
+ *   x            [rows][width] f32 or f16 activations, row stride ld_x elements;
+ *   x_packed     [rows][width] int8 codes == [rows][width/4] int32 words, the
+ *                first code in the lowest byte;
+ *   w_packed     [columns][width] int8 == [columns][width/4] int32 words
+ *                (byte-identical to the checkpoint's row-major int8 [out][in]);
+ *   w_scale      [columns] f32, w_zero [columns] int32;
+ *   out          [rows][columns].
+ */
+#ifndef OMNI_INT8_H
+#define OMNI_INT8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum omni_status {
+    OMNI_OK = 0,
+    OMNI_NOT_HANDLED = 1,
+    OMNI_NO_DEVICE = 2,
+    OMNI_BAD_ARGUMENT = 3,
+    OMNI_HIP_ERROR = -1,
+};
+
+enum omni_dtype {
+    OMNI_F32 = 0,
+    OMNI_F16 = 1,
+};
+
+/* W8A8 GEMM lowering selection for omni_w8a8_gemm / omni_try_int8_gemm.
+ * Replaces crates/omni-kernel/src/int8_tensorops.rs:15-24 (matmul2d_lowered /
+ * enabled: OMNI_CONVROT_TENSOROPS=0 forces the scalar kernel). Here the
+ * environment variable OMNI_INT8_FORCE_SCALAR=1, read once per process,
+ * forces the scalar v_dot4 kernel; otherwise the int8-MFMA kernel runs
+ * whenever width % 16 == 0 and the scalar kernel otherwise. */
+enum omni_w8a8_lowering {
+    OMNI_LOWERING_AUTO = 0,
+    OMNI_LOWERING_MFMA = 1,
+    OMNI_LOWERING_SCALAR = 2,
+};
+
+/* 1 when `device` is a gfx950 GPU, else 0; the answer is cached per device.
+ * Replaces crates/omni-kernel/src/int8_tensorops.rs:26-43 (apple10: the
+ * cached per-device family probe) and the backend check of
+ * crates/omni-kernel/src/lib.rs:32-47 (device). */
+int omni_int8_arch_supported(int device);
+
+/* Lowering that omni_w8a8_gemm would pick for this width (after the
+ * OMNI_INT8_FORCE_SCALAR override). Mirrors int8_tensorops.rs:15-20. */
+int omni_w8a8_lowering(int64_t width);
+
+/* Message for the last non-OK status returned on this thread. */
+const char* omni_int8_last_error(void);
+
+/* Per-row dynamic symmetric int8 quantisation.
+ * Replaces quantize_rows + quantize_i8, crates/omni-kernel/src/int8_matmul.rs:23-118
+ * (host twin: crates/omni-kernel/src/int8_host.rs:31-39):
+ *   row_scale = max(max|x| / 127, 1e-30); code = round-half-away(x / row_scale)
+ *   clamped to [-128, 127]; x_sum[row] = sum of the row's codes.
+ * x_dtype is OMNI_F32 or OMNI_F16 (the reference casts f16 to f32 first,
+ * int8_matmul.rs:525; an f16 value is exact in f32). width % 4 == 0.
+ * x_sum may be NULL. */
+int omni_int8_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t width,
+                            int64_t ld_x, int32_t* x_packed, float* x_scale, int32_t* x_sum,
+                            void* stream);
+
+/* W8A8 int8 x int8 -> int32 GEMM with the fused reference epilogue.
+ * Replaces int8_dot / int8_dot_tile64 / store, crates/omni-kernel/src/int8_matmul.rs:145-373:
+ *   acc[m][n] = sum_k x_packed[m][k] * w_packed[n][k]           (exact int32)
+ *   out[m][n] = f32(acc - x_sum[m] * w_zero[n]) * x_scale[m] * w_scale[n]
+ *               (+ bias[n] in f32 when bias != NULL)
+ * then stored as out_dtype (OMNI_F32: the reference's output; OMNI_F16: one
+ * round-to-nearest-even cast, what convrot.rs:91 does after the op).
+ * acc_dump, when not NULL, receives the raw int32 accumulators [rows][columns]
+ * (for bit-exact checks). width % 4 == 0; |acc| must fit in int32, which holds
+ * for width <= 131072. x_sum may be NULL only when w_zero is NULL (zero
+ * points all 0). `lowering` is an omni_w8a8_lowering value. */
+int omni_w8a8_gemm(const int32_t* x_packed, const float* x_scale, const int32_t* x_sum,
+                   const int32_t* w_packed, const float* w_scale, const int32_t* w_zero,
+                   const float* bias, int64_t rows, int64_t columns, int64_t width, void* out,
+                   int out_dtype, int32_t* acc_dump, int lowering, void* stream);
+
+/* Workspace bytes omni_try_int8_gemm needs for `rows` x `width` activations
+ * (codes, row scales and row sums, each 256-byte aligned). */
+size_t omni_try_int8_gemm_workspace_size(int64_t rows, int64_t width);
+
+/* The whole reference operator, x @ W^T after per-row int8 quantisation of x.
+ * Replaces try_int8_gemm, crates/omni-kernel/src/int8_matmul.rs:505-560
+ * (and its launch :386-471). Shape guard as :517-521: columns = scale_len;
+ * returns OMNI_NOT_HANDLED (the reference's None) unless width % 4 == 0,
+ * w_packed_len == columns * width / 4 and zero_len == columns.
+ * x [rows][width] (x_dtype f32 or f16, contiguous) -> out f32 [rows][columns]. */
+int omni_try_int8_gemm(const void* x, int x_dtype, int64_t rows, int64_t width,
+                       const int32_t* w_packed, int64_t w_packed_len, const float* w_scale,
+                       int64_t scale_len, const int32_t* w_zero, int64_t zero_len, float* out,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* Weight-only int8 linear with fp16 per-output-channel scales (W8A16).
+ * No single counterpart in the reference: it follows the reference's
+ * dequantisation convention, w_deq = w * scale, f32 accumulation
+ * (crates/omni-kernel/src/int8_matmul.rs:644-649; the weight-only CPU route
+ * crates/minicpm-v/src/quant.rs:186-200) and the decode GEMV guard style of
+ * crates/breeze-tts/src/metal_depth.rs:84-123.
+ *   out[m][n] = f16(scale[n] * sum_k x[m][k] * w[n][k] + bias[n])
+ * x f16 [rows][width], w int8 [columns][width], scale f16 [columns],
+ * bias f16 [columns] or NULL, out f16 [rows][columns]. width % 16 == 0.
+ * rows <= 16 runs the HBM-bound GEMV; larger rows run the fp16-MFMA GEMM. */
+int omni_w8a16_gemm(const uint16_t* x, const int8_t* w, const uint16_t* scale,
+                    const uint16_t* bias, int64_t rows, int64_t columns, int64_t width,
+                    uint16_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OMNI_INT8_H */

@@ -1,0 +1,236 @@
+// C ABI of libomni_int8: argument checks, the gfx950 gate and kernel dispatch.
+// Declarations and contracts: include/omni_int8.h.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+
+#include "../../include/omni_int8.h"
+#include "kernels.hpp"
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+int fail(int status, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof g_last_error, fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+int hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return OMNI_OK;
+    return fail(OMNI_HIP_ERROR, "%s: %s", what, hipGetErrorString(e));
+}
+
+// Per-device cache of the gfx950 probe: -1 unknown, 0 no, 1 yes.
+// Replaces the OnceLock<Mutex<HashMap>> of crates/omni-kernel/src/int8_tensorops.rs:26-43.
+constexpr int kMaxDevices = 64;
+int g_arch[kMaxDevices];
+std::once_flag g_arch_once;
+std::mutex g_arch_mutex;
+
+int probe_arch(int device) {
+    std::call_once(g_arch_once, [] {
+        for (int& v : g_arch) v = -1;
+    });
+    if (device < 0 || device >= kMaxDevices) return 0;
+    std::lock_guard<std::mutex> lock(g_arch_mutex);
+    if (g_arch[device] < 0) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, device) != hipSuccess) {
+            (void)hipGetLastError();
+            return 0;  // not cached: a later call may succeed
+        }
+        g_arch[device] = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+    }
+    return g_arch[device];
+}
+
+int check_current_device() {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(OMNI_NO_DEVICE, "no HIP device");
+    }
+    if (!probe_arch(device)) return fail(OMNI_NO_DEVICE, "device %d is not gfx950", device);
+    return OMNI_OK;
+}
+
+// OMNI_INT8_FORCE_SCALAR=1 forces the scalar kernel, read once per process
+// (the reference reads OMNI_CONVROT_TENSOROPS=0, int8_tensorops.rs:15-24).
+bool force_scalar() {
+    static const bool value = [] {
+        const char* v = std::getenv("OMNI_INT8_FORCE_SCALAR");
+        return v && v[0] == '1';
+    }();
+    return value;
+}
+
+bool aligned(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
+
+size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+int run_w8a8(const int32_t* x_packed, const float* x_scale, const int32_t* x_sum,
+             const int32_t* w_packed, const float* w_scale, const int32_t* w_zero,
+             const float* bias, int64_t rows, int64_t columns, int64_t width, void* out,
+             int out_dtype, int32_t* acc_dump, int lowering, hipStream_t stream) {
+    omni::W8A8Args a;
+    a.x = reinterpret_cast<const uint8_t*>(x_packed);
+    a.x_scale = x_scale;
+    a.x_sum = x_sum;
+    a.w = reinterpret_cast<const uint8_t*>(w_packed);
+    a.w_scale = w_scale;
+    a.w_zero = w_zero;
+    a.bias = bias;
+    a.out = out;
+    a.acc_dump = acc_dump;
+    a.rows = rows;
+    a.columns = columns;
+    a.width = width;
+    a.out_f16 = out_dtype == OMNI_F16;
+    int chosen = lowering == OMNI_LOWERING_AUTO ? omni_w8a8_lowering(width) : lowering;
+    if (chosen == OMNI_LOWERING_MFMA &&
+        (width % 16 != 0 || !aligned(x_packed, 16) || !aligned(w_packed, 16)))
+        chosen = OMNI_LOWERING_SCALAR;
+    if (chosen == OMNI_LOWERING_MFMA)
+        return hip_status(omni::launch_w8a8_mfma(a, stream), "w8a8 mfma launch");
+    return hip_status(omni::launch_w8a8_scalar(a, stream), "w8a8 scalar launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int omni_int8_arch_supported(int device) { return probe_arch(device); }
+
+int omni_w8a8_lowering(int64_t width) {
+    if (force_scalar()) return OMNI_LOWERING_SCALAR;
+    return width % 16 == 0 ? OMNI_LOWERING_MFMA : OMNI_LOWERING_SCALAR;
+}
+
+const char* omni_int8_last_error(void) { return g_last_error; }
+
+int omni_int8_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t width,
+                            int64_t ld_x, int32_t* x_packed, float* x_scale, int32_t* x_sum,
+                            void* stream) {
+    if (rows < 0 || width < 0 || ld_x < width)
+        return fail(OMNI_BAD_ARGUMENT, "quantize_rows: bad sizes rows=%lld width=%lld ld=%lld",
+                    (long long)rows, (long long)width, (long long)ld_x);
+    if (x_dtype != OMNI_F32 && x_dtype != OMNI_F16)
+        return fail(OMNI_BAD_ARGUMENT, "quantize_rows: unknown dtype %d", x_dtype);
+    if (width % 4 != 0) return fail(OMNI_NOT_HANDLED, "quantize_rows: width %% 4 != 0");
+    if (rows > 0 && (!x || !x_packed || !x_scale))
+        return fail(OMNI_BAD_ARGUMENT, "quantize_rows: null pointer");
+    if (!aligned(x_packed, 4)) return fail(OMNI_BAD_ARGUMENT, "quantize_rows: x_packed misaligned");
+    if (rows > 0x7fffffffLL) return fail(OMNI_BAD_ARGUMENT, "quantize_rows: too many rows");
+    int st = check_current_device();
+    if (st != OMNI_OK) return st;
+    return hip_status(omni::launch_quantize_rows(x, x_dtype == OMNI_F16, rows, width, ld_x,
+                                                 reinterpret_cast<uint8_t*>(x_packed), x_scale,
+                                                 x_sum, static_cast<hipStream_t>(stream)),
+                      "quantize_rows launch");
+}
+
+int omni_w8a8_gemm(const int32_t* x_packed, const float* x_scale, const int32_t* x_sum,
+                   const int32_t* w_packed, const float* w_scale, const int32_t* w_zero,
+                   const float* bias, int64_t rows, int64_t columns, int64_t width, void* out,
+                   int out_dtype, int32_t* acc_dump, int lowering, void* stream) {
+    if (rows < 0 || columns < 0 || width < 0)
+        return fail(OMNI_BAD_ARGUMENT, "w8a8_gemm: negative size");
+    if (out_dtype != OMNI_F32 && out_dtype != OMNI_F16)
+        return fail(OMNI_BAD_ARGUMENT, "w8a8_gemm: unknown out dtype %d", out_dtype);
+    if (lowering < OMNI_LOWERING_AUTO || lowering > OMNI_LOWERING_SCALAR)
+        return fail(OMNI_BAD_ARGUMENT, "w8a8_gemm: unknown lowering %d", lowering);
+    if (width % 4 != 0) return fail(OMNI_NOT_HANDLED, "w8a8_gemm: width %% 4 != 0");
+    if (width > 131072) return fail(OMNI_NOT_HANDLED, "w8a8_gemm: width > 131072 may overflow int32");
+    if (rows > 0 && columns > 0 &&
+        (!x_packed || !x_scale || !w_packed || !w_scale || !out || (w_zero && !x_sum)))
+        return fail(OMNI_BAD_ARGUMENT, "w8a8_gemm: null pointer");
+    if (!aligned(x_packed, 4) || !aligned(w_packed, 4))
+        return fail(OMNI_BAD_ARGUMENT, "w8a8_gemm: operands must be 4-byte aligned");
+    if (((rows + 255) / 256) * ((columns + 255) / 256) > 0x7fffffffLL || rows > 0x7fffffffLL * 4)
+        return fail(OMNI_BAD_ARGUMENT, "w8a8_gemm: problem too large");
+    int st = check_current_device();
+    if (st != OMNI_OK) return st;
+    return run_w8a8(x_packed, x_scale, x_sum, w_packed, w_scale, w_zero, bias, rows, columns,
+                    width, out, out_dtype, acc_dump, lowering, static_cast<hipStream_t>(stream));
+}
+
+size_t omni_try_int8_gemm_workspace_size(int64_t rows, int64_t width) {
+    if (rows < 0 || width < 0) return 0;
+    return round_up((size_t)rows * (size_t)width, 256) + round_up((size_t)rows * 4, 256) +
+           round_up((size_t)rows * 4, 256);
+}
+
+int omni_try_int8_gemm(const void* x, int x_dtype, int64_t rows, int64_t width,
+                       const int32_t* w_packed, int64_t w_packed_len, const float* w_scale,
+                       int64_t scale_len, const int32_t* w_zero, int64_t zero_len, float* out,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+    // Shape guard of try_int8_gemm, crates/omni-kernel/src/int8_matmul.rs:517-521.
+    const int64_t columns = scale_len;
+    if (rows < 0 || width < 0 || columns < 0)
+        return fail(OMNI_BAD_ARGUMENT, "try_int8_gemm: negative size");
+    if (width % 4 != 0 || w_packed_len != columns * width / 4 || zero_len != columns)
+        return fail(OMNI_NOT_HANDLED,
+                    "try_int8_gemm: shapes disagree (width=%lld packed=%lld columns=%lld zero=%lld)",
+                    (long long)width, (long long)w_packed_len, (long long)columns,
+                    (long long)zero_len);
+    if (x_dtype != OMNI_F32 && x_dtype != OMNI_F16)
+        return fail(OMNI_BAD_ARGUMENT, "try_int8_gemm: unknown dtype %d", x_dtype);
+    if (workspace_bytes < omni_try_int8_gemm_workspace_size(rows, width))
+        return fail(OMNI_BAD_ARGUMENT, "try_int8_gemm: workspace of %zu bytes, need %zu",
+                    workspace_bytes, omni_try_int8_gemm_workspace_size(rows, width));
+    if (rows == 0 || columns == 0) return OMNI_OK;
+    if (!x || !w_packed || !w_scale || !w_zero || !out || !workspace)
+        return fail(OMNI_BAD_ARGUMENT, "try_int8_gemm: null pointer");
+    if (!aligned(workspace, 256)) return fail(OMNI_BAD_ARGUMENT, "try_int8_gemm: workspace must be 256-byte aligned");
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    int32_t* x_packed = reinterpret_cast<int32_t*>(ws);
+    float* x_scale = reinterpret_cast<float*>(ws + round_up((size_t)rows * width, 256));
+    int32_t* x_sum = reinterpret_cast<int32_t*>(ws + round_up((size_t)rows * width, 256) +
+                                                round_up((size_t)rows * 4, 256));
+    int st = omni_int8_quantize_rows(x, x_dtype, rows, width, width, x_packed, x_scale, x_sum,
+                                     stream);
+    if (st != OMNI_OK) return st;
+    return omni_w8a8_gemm(x_packed, x_scale, x_sum, w_packed, w_scale, w_zero, nullptr, rows,
+                          columns, width, out, OMNI_F32, nullptr, OMNI_LOWERING_AUTO, stream);
+}
+
+int omni_w8a16_gemm(const uint16_t* x, const int8_t* w, const uint16_t* scale,
+                    const uint16_t* bias, int64_t rows, int64_t columns, int64_t width,
+                    uint16_t* out, void* stream) {
+    if (rows < 0 || columns < 0 || width < 0)
+        return fail(OMNI_BAD_ARGUMENT, "w8a16_gemm: negative size");
+    if (width % 16 != 0) return fail(OMNI_NOT_HANDLED, "w8a16_gemm: width %% 16 != 0");
+    if (rows == 0 || columns == 0) return OMNI_OK;
+    if (!x || !w || !scale || !out) return fail(OMNI_BAD_ARGUMENT, "w8a16_gemm: null pointer");
+    if (!aligned(x, 16) || !aligned(w, 16))
+        return fail(OMNI_BAD_ARGUMENT, "w8a16_gemm: x and w must be 16-byte aligned");
+    if (((rows + 63) / 64) * ((columns + 63) / 64) > 0x7fffffffLL)
+        return fail(OMNI_BAD_ARGUMENT, "w8a16_gemm: problem too large");
+    int st = check_current_device();
+    if (st != OMNI_OK) return st;
+    omni::W8A16Args a;
+    a.x = reinterpret_cast<const _Float16*>(x);
+    a.w = w;
+    a.scale = reinterpret_cast<const _Float16*>(scale);
+    a.bias = reinterpret_cast<const _Float16*>(bias);
+    a.out = reinterpret_cast<_Float16*>(out);
+    a.rows = rows;
+    a.columns = columns;
+    a.width = width;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // The GEMV keeps its slice of x in registers: 4 chunks of 16 per lane
+    // cover width <= 16384.
+    if (rows <= 4 && width <= 16384)
+        return hip_status(omni::launch_w8a16_gemv(a, s), "w8a16 gemv launch");
+    return hip_status(omni::launch_w8a16_mfma(a, s), "w8a16 mfma launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,42 @@
+// Host-side launchers of the gfx950 kernels (internal to libomni_int8).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace omni {
+
+hipError_t launch_quantize_rows(const void* x, bool x_is_f16, int64_t rows, int64_t width,
+                                int64_t ld, uint8_t* codes, float* scale, int32_t* sum,
+                                hipStream_t stream);
+
+struct W8A8Args {
+    const uint8_t* x;      // [rows][width] int8 codes
+    const float* x_scale;  // [rows]
+    const int32_t* x_sum;  // [rows] or null when w_zero is null
+    const uint8_t* w;      // [columns][width] int8
+    const float* w_scale;  // [columns]
+    const int32_t* w_zero; // [columns] or null (all zero)
+    const float* bias;     // [columns] or null
+    void* out;             // [rows][columns] f32 or f16
+    int32_t* acc_dump;     // [rows][columns] or null
+    int64_t rows, columns, width;
+    bool out_f16;
+};
+
+hipError_t launch_w8a8_mfma(const W8A8Args& a, hipStream_t stream);
+hipError_t launch_w8a8_scalar(const W8A8Args& a, hipStream_t stream);
+
+struct W8A16Args {
+    const _Float16* x;      // [rows][width]
+    const int8_t* w;        // [columns][width]
+    const _Float16* scale;  // [columns]
+    const _Float16* bias;   // [columns] or null
+    _Float16* out;          // [rows][columns]
+    int64_t rows, columns, width;
+};
+
+hipError_t launch_w8a16_gemv(const W8A16Args& a, hipStream_t stream);
+hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream);
+
+}  // namespace omni

@@ -1,0 +1,194 @@
+"""MI355X (gfx950) int8 quantised matmul — host-side mirror of omni-rs's operator API.
+
+The functions here keep the reference operator's names, argument meaning and
+``None`` convention and hand device tensors to libomni_int8.so through its C
+ABI. Every op runs the hand-written HIP kernels; nothing falls back to a CPU
+path: a missing library, a non-gfx950 device or a CPU tensor raises.
+
+Reference interface (GoooIce/omni-rs):
+  try_int8_gemm            crates/omni-kernel/src/int8_matmul.rs:505-560
+  Int8Linear / hadamard    crates/qwen-image/src/convrot.rs:70-160 (see convrot.py)
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import (OMNI_F16, OMNI_F32, OMNI_LOWERING_AUTO, OMNI_LOWERING_MFMA,
+                   OMNI_LOWERING_SCALAR, OMNI_NOT_HANDLED, OMNI_OK, OmniError)
+
+__all__ = [
+    "try_int8_gemm", "quantize_rows", "w8a8_gemm", "w8a16_linear", "pack_i8",
+    "arch_supported", "lowering", "OmniError",
+    "OMNI_LOWERING_AUTO", "OMNI_LOWERING_MFMA", "OMNI_LOWERING_SCALAR",
+]
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_gpu(*tensors: Optional[torch.Tensor]) -> torch.device:
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise OmniError(_lib.OMNI_BAD_ARGUMENT, "tensors must live on the GPU")
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            # crates/omni-kernel/src/lib.rs:83-88 asserts one device for all inputs
+            raise OmniError(_lib.OMNI_BAD_ARGUMENT, "tensors live on different devices")
+    if device is None:
+        raise OmniError(_lib.OMNI_BAD_ARGUMENT, "no tensor given")
+    return device
+
+
+def arch_supported(device: int = 0) -> bool:
+    """gfx950 probe, cached per device (int8_tensorops.rs:26-43 analog)."""
+    return bool(_lib.lib().omni_int8_arch_supported(device))
+
+
+def lowering(width: int) -> int:
+    """W8A8 lowering the library picks for this width (int8_tensorops.rs:15-20 analog)."""
+    return _lib.lib().omni_w8a8_lowering(width)
+
+
+def pack_i8(codes: torch.Tensor) -> torch.Tensor:
+    """Four int8 codes per int32 word, first code in the lowest byte
+    (crates/qwen-image/src/convrot.rs:151-160). Byte-identical to the codes, so
+    this is a reinterpretation, not a copy."""
+    if codes.dtype != torch.int8 or codes.numel() % 4:
+        raise ValueError("pack_i8 wants int8 codes, a multiple of 4 of them")
+    return codes.contiguous().view(torch.int32).reshape(-1)
+
+
+def quantize_rows(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Per-row symmetric int8 quantisation (int8_matmul.rs:23-118).
+
+    x: [rows, width] f32 or f16 on the GPU -> (codes int8 [rows, width],
+    row_scale f32 [rows], row_sum int32 [rows])."""
+    if x.dim() != 2:
+        raise ValueError("x must be 2-D")
+    device = _require_gpu(x)
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    rows, width = x.shape
+    dtype = {torch.float32: OMNI_F32, torch.float16: OMNI_F16}.get(x.dtype)
+    if dtype is None:
+        x = x.float()
+        dtype = OMNI_F32
+    words = torch.empty((rows, width // 4), dtype=torch.int32, device=device)
+    scale = torch.empty(rows, dtype=torch.float32, device=device)
+    total = torch.empty(rows, dtype=torch.int32, device=device)
+    st = _lib.check(_lib.lib().omni_int8_quantize_rows(
+        _ptr(x), dtype, rows, width, x.stride(0), _ptr(words), _ptr(scale), _ptr(total),
+        _stream(device)))
+    if st == OMNI_NOT_HANDLED:
+        raise ValueError(_lib.last_error())
+    return words.view(torch.int8).reshape(rows, width), scale, total
+
+
+def w8a8_gemm(codes: torch.Tensor, row_scale: torch.Tensor, row_sum: Optional[torch.Tensor],
+              w: torch.Tensor, w_scale: torch.Tensor, w_zero: Optional[torch.Tensor] = None,
+              bias: Optional[torch.Tensor] = None, out_dtype: torch.dtype = torch.float32,
+              acc_dump: bool = False, lowering: int = OMNI_LOWERING_AUTO):
+    """int8 x int8 -> int32 GEMM with the fused reference epilogue
+    (int8_matmul.rs:145-373). codes int8 [rows, width]; w int8 [columns, width]
+    (or its packed int32 words); w_scale f32 [columns]; w_zero int32 [columns];
+    bias f32 [columns]. Returns out (and the int32 accumulators if acc_dump)."""
+    device = _require_gpu(codes, row_scale, row_sum, w, w_scale, w_zero, bias)
+    rows, width = codes.shape
+    if w.dtype == torch.int32:
+        w = w.view(torch.int8)
+    w = w.reshape(-1, width) if w.numel() else w.reshape(0, width)
+    columns = w.shape[0]
+    for t, n, dt in ((row_scale, rows, torch.float32), (w_scale, columns, torch.float32)):
+        if t.numel() != n or t.dtype != dt:
+            raise ValueError("scale shape/dtype mismatch")
+    if w_zero is not None and (w_zero.numel() != columns or w_zero.dtype != torch.int32):
+        raise ValueError("w_zero must be int32 [columns]")
+    if bias is not None and (bias.numel() != columns or bias.dtype != torch.float32):
+        raise ValueError("bias must be f32 [columns]")
+    odt = {torch.float32: OMNI_F32, torch.float16: OMNI_F16}[out_dtype]
+    out = torch.empty((rows, columns), dtype=out_dtype, device=device)
+    acc = torch.empty((rows, columns), dtype=torch.int32, device=device) if acc_dump else None
+    st = _lib.check(_lib.lib().omni_w8a8_gemm(
+        _ptr(codes.contiguous()), _ptr(row_scale), _ptr(row_sum), _ptr(w.contiguous()),
+        _ptr(w_scale), _ptr(w_zero), _ptr(bias), rows, columns, width, _ptr(out), odt, _ptr(acc),
+        lowering, _stream(device)))
+    if st == OMNI_NOT_HANDLED:
+        raise ValueError(_lib.last_error())
+    return (out, acc) if acc_dump else out
+
+
+def try_int8_gemm(x: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor,
+                  w_zero: torch.Tensor) -> Optional[torch.Tensor]:
+    """``x @ W^T`` after per-row symmetric int8 quantisation of ``x``.
+
+    Mirrors ``omni_kernel::int8_matmul::try_int8_gemm``
+    (crates/omni-kernel/src/int8_matmul.rs:505-560): ``w_packed`` holds
+    ``n * (k / 4)`` little-endian int8 groups; ``w_scale`` and ``w_zero`` are
+    per output row. Returns an f32 ``[rows, n]`` tensor, or ``None`` when the
+    shapes disagree (:517-521). Float inputs of any dtype are cast to f32
+    (:525-526; f16 is passed through, since it is exact in f32); integer
+    inputs may be int32 or int64 (int64 is truncated to int32 as read_i32,
+    :587-595, does)."""
+    rows, width = x.shape
+    columns = w_scale.shape[0]
+    if width % 4 != 0 or w_packed.shape[0] != columns * width // 4 or w_zero.shape[0] != columns:
+        return None
+    device = _require_gpu(x, w_packed, w_scale, w_zero)
+    if x.dtype not in (torch.float32, torch.float16):
+        x = x.float()
+    x = x.contiguous()
+    w_packed = w_packed.to(torch.int32).contiguous()
+    w_scale = w_scale.to(torch.float32).contiguous()
+    w_zero = w_zero.to(torch.int32).contiguous()
+    L = _lib.lib()
+    ws_bytes = L.omni_try_int8_gemm_workspace_size(rows, width)
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    out = torch.empty((rows, columns), dtype=torch.float32, device=device)
+    st = _lib.check(L.omni_try_int8_gemm(
+        _ptr(x), OMNI_F16 if x.dtype == torch.float16 else OMNI_F32, rows, width,
+        _ptr(w_packed), w_packed.shape[0], _ptr(w_scale), columns, _ptr(w_zero), columns,
+        _ptr(out), _ptr(workspace), ws_bytes, _stream(device)))
+    if st == OMNI_NOT_HANDLED:
+        return None
+    return out
+
+
+def w8a16_linear(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor,
+                 bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Weight-only int8 linear: f16(scale[n] * sum_k x[m,k] * w[n,k] + bias[n]).
+
+    x f16 [rows, width] (leading dims are flattened), w int8 [columns, width],
+    scale/bias f16 [columns] -> f16 [..., columns]. Decode shapes (rows <= 4)
+    run the HBM-bound GEMV, larger ones the fp16-MFMA GEMM."""
+    lead = x.shape[:-1]
+    width = x.shape[-1]
+    x2 = x.reshape(-1, width)
+    device = _require_gpu(x2, w, scale, bias)
+    if x2.dtype != torch.float16 or w.dtype != torch.int8 or scale.dtype != torch.float16:
+        raise ValueError("w8a16_linear wants f16 x, int8 w, f16 scale")
+    if bias is not None and bias.dtype != torch.float16:
+        raise ValueError("bias must be f16")
+    columns = w.shape[0]
+    if w.shape[1] != width or scale.numel() != columns or (bias is not None and bias.numel() != columns):
+        raise ValueError("w8a16_linear: shapes disagree")
+    x2 = x2.contiguous()
+    w = w.contiguous()
+    out = torch.empty((x2.shape[0], columns), dtype=torch.float16, device=device)
+    st = _lib.check(_lib.lib().omni_w8a16_gemm(
+        _ptr(x2), _ptr(w), _ptr(scale.contiguous()), _ptr(None if bias is None else bias.contiguous()),
+        x2.shape[0], columns, width, _ptr(out), _stream(device)))
+    if st == OMNI_NOT_HANDLED:
+        raise ValueError(_lib.last_error())
+    return out.reshape(*lead, columns)

@@ -1,0 +1,122 @@
+"""Weight-only int8 (W8A16) parity on the GPU.
+
+The reference has no W8A16 op; its dequantisation convention (w * scale per
+output channel, f32 accumulation, int8_matmul.rs:644-649 / quant.rs:186-200)
+is restated by the oracle. The bar is the north_star one: max relative error
+<= 1e-2 with fp16 output (tests/tolerance.py), against the f64 ground truth
+and against the oracle's dequantise-to-f16 route. The fp16-GEMV analog test
+of the reference (crates/breeze-tts/src/metal_depth_tests.rs:16-80) sweeps
+small and odd shapes the same way.
+"""
+import numpy as np
+import pytest
+import torch
+
+import omni_int8 as oi
+import tolerance
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    assert oi.arch_supported(torch.cuda.current_device()), "device is not gfx950"
+
+
+def make(rng, rows, width, columns, bias=False):
+    x = rng.standard_normal((rows, width)).astype(np.float16)
+    w = rng.integers(-127, 128, (columns, width), dtype=np.int8)
+    s = rng.uniform(0.002, 0.02, columns).astype(np.float16)
+    b = rng.standard_normal(columns).astype(np.float16) if bias else None
+    return x, w, s, b
+
+
+def gpu_f64_reference(x, w, s, b):
+    """Full-size ground truth on the GPU in f64 (products of f16 and int8 are
+    exact in f64; the sum carries ~1e-16 relative error)."""
+    ref = dev(x).double() @ dev(w).double().T
+    ref = ref * dev(s).double()[None, :]
+    if b is not None:
+        ref = ref + dev(b).double()[None, :]
+    return host(ref)
+
+
+@pytest.mark.parametrize("rows", [1, 2, 3, 4])
+@pytest.mark.parametrize("width,columns", [(16, 1), (32, 7), (256, 33), (4096, 100), (4112, 9),
+                                          (8192, 1024), (16384, 65)])
+def test_gemv_small_and_odd_shapes(oracle, rows, width, columns):
+    rng = np.random.default_rng(rows * 31 + width + columns)
+    x, w, s, b = make(rng, rows, width, columns, bias=columns % 2 == 1)
+    got = host(oi.w8a16_linear(dev(x), dev(w), dev(s), None if b is None else dev(b)))
+    ref = oracle.w8a16_f64(x, w, s, b)
+    assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL
+    route = oracle.w8a16_gemm(x, w, s, b)
+    assert tolerance.rel_err(got, route.astype(np.float64)) <= tolerance.FP16_REL_TOL
+
+
+def test_gemv_exact_on_integer_inputs():
+    # integer x, scale 1: every partial sum is an integer below 2^11 -> exact
+    x = np.tile(np.arange(-4, 4, dtype=np.float16), (4, 64))[:, :512].copy()
+    x = x.reshape(4, 512)
+    w = ((np.arange(9 * 512) % 5) - 2).astype(np.int8).reshape(9, 512)
+    s = np.ones(9, np.float16)
+    got = host(oi.w8a16_linear(dev(x), dev(w), dev(s)))
+    want = (x.astype(np.int64) @ w.astype(np.int64).T).astype(np.float16)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("rows", [1, 4])
+@pytest.mark.parametrize("width,columns", [(4096, 4096), (4096, 14336), (14336, 4096),
+                                          (4096, 128256)])
+def test_config2_decode_sweep_full_size(oracle, rows, width, columns):
+    # 7B-LLM decode shapes, M = 1 and 4
+    rng = np.random.default_rng(width + columns + rows)
+    x, w, s, b = make(rng, rows, width, columns)
+    got = host(oi.w8a16_linear(dev(x), dev(w), dev(s)))
+    ref = gpu_f64_reference(x, w, s, b)
+    assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL
+    cols = rng.choice(columns, 64, replace=False)
+    route = oracle.w8a16_gemm(x, w[cols], s[cols])
+    assert tolerance.rel_err(got[:, cols], route.astype(np.float64)) <= tolerance.FP16_REL_TOL
+
+
+def test_config1_reference_cpu_case(oracle):
+    # M=16, K=4096, N=4096, seed 0 (GEMM path at M=16)
+    rng = np.random.default_rng(0)
+    x, w, s, _ = make(rng, 16, 4096, 4096)
+    got = host(oi.w8a16_linear(dev(x), dev(w), dev(s)))
+    ref = oracle.w8a16_f64(x, w, s)
+    assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL
+
+
+@pytest.mark.parametrize("rows,width,columns", [(5, 64, 33), (16, 256, 64), (17, 1536, 1536),
+                                                (64, 8960, 1536), (130, 1536, 8960),
+                                                (1024, 1536, 2048), (33, 20000, 40)])
+def test_mfma_gemm_shapes(oracle, rows, width, columns):
+    rng = np.random.default_rng(rows + width + columns)
+    x, w, s, b = make(rng, rows, width, columns, bias=True)
+    got = host(oi.w8a16_linear(dev(x), dev(w), dev(s), dev(b)))
+    ref = gpu_f64_reference(x, w, s, b)
+    assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL
+
+
+def test_config5_small_vlm_layer(oracle):
+    # BASELINE config 5, one layer: prefill M=1024 then a decode step M=1
+    rng = np.random.default_rng(5)
+    hidden, ffn = 1536, 8960
+    for rows in (1024, 1):
+        for width, columns in ((hidden, hidden), (hidden, 512), (hidden, ffn), (ffn, hidden)):
+            x, w, s, _ = make(rng, rows, width, columns)
+            got = host(oi.w8a16_linear(dev(x), dev(w), dev(s)))
+            ref = gpu_f64_reference(x, w, s, None)
+            assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL, (rows, width, columns)

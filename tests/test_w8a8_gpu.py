@@ -1,0 +1,215 @@
+"""W8A8 parity on the GPU: the HIP kernels against the CPU oracle (bit-exact).
+
+Mirrors the reference's own tests — crates/omni-kernel/src/int8_matmul.rs:700-786
+(hand value, 64^3 tile fixture, negative control, both lowerings) and
+prototypes/int8-gemm/src/main.rs:69-89 (check shapes) — then covers the
+BASELINE configs at full size. Integer accumulators and the f32 epilogue are
+compared for exact equality; nothing here has a tolerance except where the
+reference's own test has one.
+"""
+import numpy as np
+import pytest
+import torch
+
+import omni_int8 as oi
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    assert oi.arch_supported(torch.cuda.current_device()), "device is not gfx950"
+
+
+def weights(rng, columns, width):
+    return rng.integers(-127, 128, (columns, width), dtype=np.int8)
+
+
+def run_gemm(x, w, scale, zero, lowering=oi.OMNI_LOWERING_AUTO, bias=None, out_dtype=torch.float32):
+    codes, rs, total = oi.quantize_rows(dev(x))
+    out, acc = oi.w8a8_gemm(codes, rs, total, dev(w), dev(scale), dev(zero),
+                            bias=None if bias is None else dev(bias), out_dtype=out_dtype,
+                            acc_dump=True, lowering=lowering)
+    return host(codes), host(rs), host(total), host(out), host(acc)
+
+
+# -- quantisation ----------------------------------------------------------------
+
+
+@pytest.mark.parametrize("rows,width", [(1, 4), (3, 12), (17, 36), (5, 100), (64, 4096),
+                                        (7, 12288), (2, 4100)])
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_quantize_rows_bit_exact(oracle, rows, width, dtype):
+    rng = np.random.default_rng(rows * 1000 + width)
+    x = rng.standard_normal((rows, width)).astype(dtype)
+    if rows > 2:
+        x[1] = 0  # zero row: the 1e-30 floor
+    codes, rs, total = oi.quantize_rows(dev(x))
+    ocodes, ors, ototal = oracle.quantize_rows(x.astype(np.float32))
+    assert np.array_equal(host(codes), ocodes)
+    assert np.array_equal(host(rs).view(np.uint32), ors.view(np.uint32))
+    assert np.array_equal(host(total), ototal)
+
+
+def test_quantize_rows_ties_and_strided_input(oracle):
+    # peak 127 -> row_scale 1: exact half-way quotients, and the f32 add in
+    # floor(|q| + 0.5) that sends 0.49999997 to 1 (int8_matmul.rs:106).
+    row = np.array([127.0, 2.5, -2.5, 0.5, -0.5, 126.5, -126.5, 0.49999997, -0.49999997, 1.5,
+                    -1.5, 0.0], np.float32)
+    x = np.tile(row, (3, 1))
+    big = np.zeros((3, 20), np.float32)
+    big[:, :12] = x
+    strided = dev(big)[:, :12]  # leading dimension 20
+    codes, rs, total = oi.quantize_rows(strided)
+    assert host(codes)[0].tolist() == [127, 3, -3, 1, -1, 127, -127, 1, -1, 2, -2, 0]
+    ocodes, _, ototal = oracle.quantize_rows(x)
+    assert np.array_equal(host(codes), ocodes) and np.array_equal(host(total), ototal)
+
+
+# -- the reference's own tests ------------------------------------------------------
+
+
+@pytest.mark.parametrize("lowering", [oi.OMNI_LOWERING_AUTO, oi.OMNI_LOWERING_SCALAR])
+def test_hand_value_and_tile64_fixture(oracle, lowering):
+    # int8_matmul.rs:749-786: hand value on the scalar kernel, then the 64^3
+    # tile fixture on both lowerings, with the got+1 negative control.
+    x = np.array([[1.0, -2.0, 0.5, 4.0]], np.float32)
+    w = np.array([[1, -2, 3, -4]], np.int8)
+    scale, zero = np.array([0.25], np.float32), np.array([1], np.int32)
+    expected = oracle.dequant_reference(x, w, scale, zero)
+    assert abs(expected[0, 0] - (-411.0 / 127.0)) < 1e-5
+    got = host(oi.try_int8_gemm(dev(x), dev(oracle.pack_i8(w)), dev(scale), dev(zero)))
+    assert np.max(np.abs(got - expected)) < 1e-3
+    assert abs(got[0, 0] + 1.0 - expected[0, 0]) >= 1e-3
+
+    x = np.zeros((64, 64), np.float32)
+    x[0, :4] = [1.0, -2.0, 0.5, 4.0]
+    w = np.zeros((64, 64), np.int8)
+    w[0, :4] = [1, -2, 3, -4]
+    scale = np.full(64, 0.25, np.float32)
+    zero = np.zeros(64, np.int32)
+    zero[0] = 1
+    expected = oracle.dequant_reference(x, w, scale, zero)
+    *_, out, acc = run_gemm(x, w, scale, zero, lowering=lowering)
+    assert np.max(np.abs(out - expected)) < 1e-3
+    assert abs(out[0, 0] + 1.0 - expected[0, 0]) >= 1e-3
+    assert np.array_equal(out, oracle.int8_gemm(x, w, scale, zero))
+
+
+@pytest.mark.parametrize("rows,width,columns", [(5, 12, 6), (17, 36, 14)])
+def test_prototype_check_shapes(oracle, rows, width, columns):
+    # prototypes/int8-gemm/src/main.rs:69-89 (widths not a multiple of 16: scalar lowering)
+    i = np.arange(rows * width)
+    x = (((i * 17) % 41) - 20).astype(np.float32).reshape(rows, width)
+    w = (((np.arange(columns * width) * 13) % 31) - 15).astype(np.int8).reshape(columns, width)
+    scale = (0.05 + np.arange(columns, dtype=np.float32) * 0.01).astype(np.float32)
+    zero = ((np.arange(columns) % 5) - 2).astype(np.int32)
+    got = host(oi.try_int8_gemm(dev(x), dev(oracle.pack_i8(w)), dev(scale), dev(zero)))
+    want = oracle.int8_gemm(x, w, scale, zero)
+    assert np.max(np.abs(got - want)) < 1e-3       # the prototype's bar
+    assert np.array_equal(got, want)               # and in fact bit-exact
+
+
+def test_try_int8_gemm_returns_none_on_shape_mismatch():
+    x = torch.zeros((2, 8), device="cuda")
+    assert oi.try_int8_gemm(x, torch.zeros(3, dtype=torch.int32, device="cuda"),
+                            torch.ones(2, device="cuda"), torch.zeros(2, dtype=torch.int32, device="cuda")) is None
+    assert oi.try_int8_gemm(torch.zeros((2, 6), device="cuda"), torch.zeros(3, dtype=torch.int32, device="cuda"),
+                            torch.ones(2, device="cuda"), torch.zeros(2, dtype=torch.int32, device="cuda")) is None
+
+
+# -- both lowerings, ragged shapes, epilogue variants ------------------------------------
+
+
+SHAPES = [(1, 16, 1), (1, 64, 7), (3, 48, 5), (64, 64, 64), (255, 208, 129), (257, 4112, 300),
+          (300, 512, 513), (16, 1024, 2048)]
+
+
+@pytest.mark.parametrize("rows,width,columns", SHAPES)
+@pytest.mark.parametrize("lowering", [oi.OMNI_LOWERING_MFMA, oi.OMNI_LOWERING_SCALAR])
+def test_w8a8_bit_exact_ragged(oracle, rows, width, columns, lowering):
+    rng = np.random.default_rng(rows + 7 * width + 13 * columns)
+    x = rng.standard_normal((rows, width)).astype(np.float32)
+    w = rng.integers(-128, 128, (columns, width), dtype=np.int8)
+    scale = rng.uniform(0.002, 0.02, columns).astype(np.float32)
+    zero = rng.integers(-4, 5, columns).astype(np.int32)
+    bias = rng.standard_normal(columns).astype(np.float32)
+    codes, rs, total, out, acc = run_gemm(x, w, scale, zero, lowering=lowering)
+    oacc = oracle.int8_acc(codes, w)
+    assert np.array_equal(acc, oacc)
+    o32, _ = oracle.w8a8_finish(oacc, total, rs, scale, zero)
+    assert np.array_equal(out.view(np.uint32), o32.view(np.uint32))
+    # fp16 output with bias: one RNE rounding of the f32 value + bias
+    *_, out16, _ = run_gemm(x, w, scale, zero, lowering=lowering, bias=bias, out_dtype=torch.float16)
+    _, o16 = oracle.w8a8_finish(oacc, total, rs, scale, zero, bias)
+    assert np.array_equal(out16.view(np.uint16), o16)
+
+
+def test_w8a8_extreme_codes_no_overflow(oracle):
+    # |acc| = 128 * 128 * K at K = 16384 is 2^28: exact in int32
+    width = 16384
+    x = np.full((3, width), -1.0, np.float32)
+    x[:, 0] = 1.0  # codes: -127 mostly
+    w = np.full((40, width), -128, np.int8)
+    scale = np.full(40, 0.01, np.float32)
+    zero = np.zeros(40, np.int32)
+    codes, rs, total, out, acc = run_gemm(x, w, scale, zero, lowering=oi.OMNI_LOWERING_MFMA)
+    assert np.array_equal(acc, oracle.int8_acc(codes, w))
+
+
+# -- BASELINE configs at full size ---------------------------------------------------
+
+
+def full_size_check(oracle, rows, width, columns, seed, outliers=False, sample_rows=12):
+    """Full-size check: the int32 accumulators against an exact f64 GEMM on the
+    GPU (integers below 2^53, so f64 is exact), the f32 epilogue against the
+    reference op order in torch f32, and sampled rows against the C oracle."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((rows, width)).astype(np.float16)
+    if outliers:  # 1% of channels x20 (diffusion config)
+        ch = rng.choice(width, size=max(1, width // 100), replace=False)
+        x[:, ch] = (x[:, ch].astype(np.float32) * 20).astype(np.float16)
+    w = rng.integers(-127, 128, (columns, width), dtype=np.int8)
+    scale = rng.uniform(0.002, 0.02, columns).astype(np.float32)
+    zero = np.zeros(columns, np.int32)
+    zero[::7] = 3  # a nonzero-zero-point parity case on every 7th channel
+    xd, wd = dev(x), dev(w)
+    codes, rs, total = oi.quantize_rows(xd)
+    out, acc = oi.w8a8_gemm(codes, rs, total, wd, dev(scale), dev(zero), acc_dump=True)
+    exact = (codes.double() @ wd.double().T)
+    assert torch.equal(acc.double(), exact)
+    centered = acc - total[:, None] * dev(zero)[None, :]
+    ref = (centered.float() * rs[:, None]) * dev(scale)[None, :]
+    assert torch.equal(out.view(torch.int32), ref.view(torch.int32))
+    # sampled rows through the C oracle from the f16 input (quantisation included)
+    idx = np.unique(np.concatenate([[0, rows - 1], rng.choice(rows, sample_rows, replace=False)]))
+    want = oracle.int8_gemm(x[idx].astype(np.float32), w, scale, zero)
+    got = host(out)[idx]
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("columns", [4096, 14336])
+def test_config3_prefill_full_size(oracle, columns):
+    # M = 4 x 512, K = 4096
+    full_size_check(oracle, 2048, 4096, columns, seed=columns)
+
+
+@pytest.mark.parametrize("width,columns", [(3072, 9216), (3072, 12288), (12288, 3072)])
+def test_config4_diffusion_full_size(oracle, width, columns):
+    # M = 4096 + 256 tokens, 1% outlier channels x20
+    full_size_check(oracle, 4352, width, columns, seed=width + columns, outliers=True, sample_rows=6)
+
+
+@pytest.mark.parametrize("width,columns", [(3072, 12288), (12288, 3072)])
+def test_north_star_gemm_full_size(oracle, width, columns):
+    full_size_check(oracle, 4096, width, columns, seed=7, sample_rows=6)

@@ -1,0 +1,24 @@
+"""The floating-point bar for the dequantised (fp16-output) paths.
+
+north_star: max relative error <= 1e-2 with fp16 output. Relative error is
+taken per element against the f64 ground truth, with the denominator floored
+at 0.1 x the RMS of the reference outputs: outputs are sums of thousands of
+signed terms, so some land near zero where any change of summation order is
+an unbounded *relative* change (the reference's own GEMV/W4A16 tests floor
+their denominators too, crates/minicpm-v/src/quant.rs:313,552).
+"""
+import numpy as np
+
+FP16_REL_TOL = 1e-2
+
+
+def rel_err(got, ref):
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    if ref.size == 0:
+        return 0.0
+    if not np.all(np.isfinite(got)):
+        return float("inf")
+    rms = float(np.sqrt(np.mean(ref * ref)))
+    floor = max(0.1 * rms, 1e-30)
+    return float(np.max(np.abs(got - ref) / np.maximum(np.abs(ref), floor)))
