@@ -95,8 +95,11 @@ int run_w8a8(const int32_t* x_packed, const float* x_scale, const int32_t* x_sum
     a.width = width;
     a.out_f16 = out_dtype == OMNI_F16;
     int chosen = lowering == OMNI_LOWERING_AUTO ? omni_w8a8_lowering(width) : lowering;
+    // The MFMA kernel needs 16-byte rows and keeps in-tile output offsets in
+    // 32 bits (256 * columns < 2^31).
     if (chosen == OMNI_LOWERING_MFMA &&
-        (width % 16 != 0 || !aligned(x_packed, 16) || !aligned(w_packed, 16)))
+        (width % 16 != 0 || !aligned(x_packed, 16) || !aligned(w_packed, 16) ||
+         columns >= (int64_t(1) << 23)))
         chosen = OMNI_LOWERING_SCALAR;
     if (chosen == OMNI_LOWERING_MFMA)
         return hip_status(omni::launch_w8a8_mfma(a, stream), "w8a8 mfma launch");
@@ -154,7 +157,7 @@ int omni_w8a8_gemm(const int32_t* x_packed, const float* x_scale, const int32_t*
         return fail(OMNI_BAD_ARGUMENT, "w8a8_gemm: null pointer");
     if (!aligned(x_packed, 4) || !aligned(w_packed, 4))
         return fail(OMNI_BAD_ARGUMENT, "w8a8_gemm: operands must be 4-byte aligned");
-    if (((rows + 255) / 256) * ((columns + 255) / 256) > 0x7fffffffLL || rows > 0x7fffffffLL * 4)
+    if (((rows + 255) / 256) * ((columns + 127) / 128) > 0x7fffffffLL || rows > 0x7fffffffLL)
         return fail(OMNI_BAD_ARGUMENT, "w8a8_gemm: problem too large");
     int st = check_current_device();
     if (st != OMNI_OK) return st;

@@ -6,11 +6,19 @@
 //   code      = clamp(sign(x) * floor(|x / row_scale| + 0.5), -128, 127)
 //   sum       = sum of the row's codes
 //
-// Design: one 256-lane workgroup per row. Pass 1 streams the row once for the
-// peak (wave max over DPP/shuffles, then 4 partials through LDS). Pass 2
-// streams it again — the row was just read, so this pass hits L2 — divides,
-// rounds and writes the codes as packed little-endian int8 words. HBM traffic
-// is one read of x and one write of the codes: the kernel is HBM-bound.
+// Design: one 256-lane workgroup per row. Rows of up to 16384 elements are
+// read once into registers (16-element chunks, 128-bit loads), the peak is
+// reduced across the wave and then across the 4 waves through LDS, and the
+// codes are written as packed little-endian int8 words: HBM traffic is one
+// read of x and one write of the codes. Longer or misaligned rows take a
+// two-pass variant whose second pass re-reads the row from L2.
+//
+// The division x / row_scale must be IEEE (correctly rounded): a code flips
+// when a quotient near k + 0.5 rounds the other way. It is computed as
+// q0 = x * y, r = fma(-q0, s, x), q = fma(r, y, q0) with y = RN(1 / s)
+// (Markstein's correction step), which returns RN(x / s) whenever the
+// residual r is exact; rows with s < 2^-90 (where r can leave the normal
+// range) use the hardware-expanded IEEE division instead.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -49,6 +57,161 @@ __device__ __forceinline__ void load_row_chunk(const T* __restrict__ p, float (&
     }
 }
 
+
+// RN(x / s) given y = RN(1 / s); see the file comment for when it is exact.
+__device__ __forceinline__ float div_rn(float x, float s, float y, bool tiny_scale) {
+#pragma clang fp contract(off)
+    if (tiny_scale) return x / s;
+    const float q0 = x * y;
+    const float r = __builtin_fmaf(-q0, s, x);
+    return __builtin_fmaf(r, y, q0);
+}
+
+// Codes of four consecutive values packed little-endian into one word.
+__device__ __forceinline__ u32 pack4(const float* v, float s, float y, bool tiny, int& sum) {
+    u32 word = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const int q = quantize_code(div_rn(v[b], s, y, tiny));
+        sum += q;
+        word |= (u32)(q & 255) << (8 * b);
+    }
+    return word;
+}
+
+// Row scale from the peak: max(peak / 127, 1e-30) (int8_matmul.rs:63-68).
+__device__ __forceinline__ float row_scale_of(float peak) {
+    float row_scale = peak / 127.0f;
+    // `!(a > b)` also catches a NaN peak, like Rust's f32::max with 1e-30.
+    if (!(row_scale > 1.0e-30f)) row_scale = 1.0e-30f;
+    return row_scale;
+}
+
+// Block-wide max of one value per thread (256 threads, 4 waves).
+__device__ __forceinline__ float block_max(float v, float* s_red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    v = wave_max(v);
+    if (lane == 0) s_red[wave] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+}
+
+// Single-read variant: each thread owns chunks tid + 256*j (j < CPT) of 16
+// elements, held in registers between the peak and the code pass.
+template <typename T, int CPT>
+__global__ __launch_bounds__(256) void quantize_rows_reg_kernel(
+    const T* __restrict__ x, int64_t width, int64_t ld, uint8_t* __restrict__ codes,
+    float* __restrict__ scale_out, int32_t* __restrict__ sum_out) {
+    __shared__ float s_peak[4];
+    __shared__ int s_sum[4];
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const T* src = x + row * ld;
+    const int chunks = (int)(width / 16);
+    float v[CPT][16];
+    float peak = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        const int c = tid + 256 * j;
+        if (c < chunks) {
+            load_row_chunk<T, 16, true>(src + (int64_t)c * 16, v[j]);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) peak = fmaxf(peak, __builtin_fabsf(v[j][i]));
+        }
+    }
+    peak = block_max(peak, s_peak);
+    const float s = row_scale_of(peak);
+    const float y = 1.0f / s;
+    const bool tiny = s < 0x1p-90f;
+    int local = 0;
+    uint8_t* dst = codes + row * width;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        const int c = tid + 256 * j;
+        if (c < chunks) {
+            uint4 w;
+            w.x = pack4(&v[j][0], s, y, tiny, local);
+            w.y = pack4(&v[j][4], s, y, tiny, local);
+            w.z = pack4(&v[j][8], s, y, tiny, local);
+            w.w = pack4(&v[j][12], s, y, tiny, local);
+            *reinterpret_cast<uint4*>(dst + (int64_t)c * 16) = w;
+        }
+    }
+    if (sum_out) {
+        local = wave_sum_i32(local);
+        if ((tid & 63) == 0) s_sum[tid >> 6] = local;
+        __syncthreads();
+        if (tid == 0) sum_out[row] = s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3];
+    }
+    if (tid == 0) scale_out[row] = s;
+}
+
+// Wave-per-row variant: each wave quantises one row on its own (no LDS, no
+// barrier), lane l owning chunks l + 64*j (j < CPW) of 16 elements, kept in
+// registers in the input type between the peak and the code pass.
+template <typename T, int CPW>
+__global__ __launch_bounds__(256) void quantize_rows_wave_kernel(
+    const T* __restrict__ x, int64_t rows, int64_t width, int64_t ld, uint8_t* __restrict__ codes,
+    float* __restrict__ scale_out, int32_t* __restrict__ sum_out) {
+    constexpr int kWords = 16 * (int)sizeof(T) / 16;  // uint4 per 16-element chunk
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;  // whole wave exits together
+    const T* src = x + row * ld;
+    const int chunks = (int)(width / 16);
+    uint4 raw[CPW][kWords];
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+        const int c = lane + 64 * j;
+        if (c < chunks) {
+#pragma unroll
+            for (int w = 0; w < kWords; ++w)
+                raw[j][w] = reinterpret_cast<const uint4*>(src + (int64_t)c * 16)[w];
+        }
+    }
+    auto unpack = [&](int j, float (&v)[16]) {
+        T tmp[16];
+        __builtin_memcpy(tmp, raw[j], sizeof(tmp));
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = to_f32(tmp[i]);
+    };
+    float peak = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+        if (lane + 64 * j < chunks) {
+            float v[16];
+            unpack(j, v);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) peak = fmaxf(peak, __builtin_fabsf(v[i]));
+        }
+    }
+    peak = wave_max(peak);
+    const float s = row_scale_of(peak);
+    const float y = 1.0f / s;
+    const bool tiny = s < 0x1p-90f;
+    int local = 0;
+    uint8_t* dst = codes + row * width;
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+        const int c = lane + 64 * j;
+        if (c < chunks) {
+            float v[16];
+            unpack(j, v);
+            uint4 w;
+            w.x = pack4(&v[0], s, y, tiny, local);
+            w.y = pack4(&v[4], s, y, tiny, local);
+            w.z = pack4(&v[8], s, y, tiny, local);
+            w.w = pack4(&v[12], s, y, tiny, local);
+            *reinterpret_cast<uint4*>(dst + (int64_t)c * 16) = w;
+        }
+    }
+    if (sum_out) {
+        local = wave_sum_i32(local);
+        if (lane == 0) sum_out[row] = local;
+    }
+    if (lane == 0) scale_out[row] = s;
+}
+
 template <typename T, int VEC, bool ALIGNED>
 __global__ __launch_bounds__(256) void quantize_rows_kernel(
     const T* __restrict__ x, int64_t width, int64_t ld, uint8_t* __restrict__ codes,
@@ -69,13 +232,10 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
 #pragma unroll
         for (int i = 0; i < VEC; ++i) peak = fmaxf(peak, __builtin_fabsf(v[i]));
     }
-    peak = wave_max(peak);
-    if (lane == 0) s_peak[wave] = peak;
-    __syncthreads();
-    peak = fmaxf(fmaxf(s_peak[0], s_peak[1]), fmaxf(s_peak[2], s_peak[3]));
-    float row_scale = peak / 127.0f;
-    // `!(a > b)` also catches a NaN peak, like Rust's f32::max with 1e-30.
-    if (!(row_scale > 1.0e-30f)) row_scale = 1.0e-30f;
+    peak = block_max(peak, s_peak);
+    const float row_scale = row_scale_of(peak);
+    const float y = 1.0f / row_scale;
+    const bool tiny = row_scale < 0x1p-90f;
 
     int local = 0;
     uint8_t* dst = codes + row * width;
@@ -84,16 +244,7 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
         load_row_chunk<T, VEC, ALIGNED>(src + c * VEC, v);
         u32 words[VEC / 4];
 #pragma unroll
-        for (int w = 0; w < VEC / 4; ++w) {
-            u32 word = 0;
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                int q = quantize_code(v[4 * w + b] / row_scale);
-                local += q;
-                word |= (u32)(q & 255) << (8 * b);
-            }
-            words[w] = word;
-        }
+        for (int w = 0; w < VEC / 4; ++w) words[w] = pack4(&v[4 * w], row_scale, y, tiny, local);
         if constexpr (ALIGNED && VEC == 16) {
             *reinterpret_cast<uint4*>(dst + c * VEC) = make_uint4(words[0], words[1], words[2], words[3]);
         } else if constexpr (ALIGNED && VEC == 8) {
@@ -137,6 +288,34 @@ hipError_t launch_typed(const T* x, int64_t rows, int64_t width, int64_t ld, uin
         const int64_t align = in_bytes >= 16 ? 16 : in_bytes;
         return base % align == 0 && (ld * (int64_t)sizeof(T)) % align == 0 && cbase % vec == 0;
     };
+    // One wave per row while the row fits in registers (16 KiB of input).
+    constexpr int64_t kWaveMax = 8192 / (int64_t)sizeof(T) * 2;  // 16384 f16, 8192 f32
+    if (width % 16 == 0 && width <= kWaveMax && aligned_for(16)) {
+        const int cpw = (int)((width / 16 + 63) / 64);
+        dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+#define OMNI_QWAVE(n) hipLaunchKernelGGL((quantize_rows_wave_kernel<T, n>), grid, block, 0, stream, x, rows, width, ld, codes, scale, sum)
+        if (cpw <= 1) OMNI_QWAVE(1);
+        else if (cpw <= 2) OMNI_QWAVE(2);
+        else if (cpw <= 3) OMNI_QWAVE(3);
+        else if (cpw <= 4) OMNI_QWAVE(4);
+        else if (cpw <= 6) OMNI_QWAVE(6);
+        else if (cpw <= 8) OMNI_QWAVE(8);
+        else if (cpw <= 12) OMNI_QWAVE(12);
+        else OMNI_QWAVE(16);
+#undef OMNI_QWAVE
+        return hipGetLastError();
+    }
+    if (width % 16 == 0 && width <= 16384 && aligned_for(16)) {
+        const int cpt = (int)((width / 16 + 255) / 256);
+        dim3 grid((unsigned)rows), block(256);
+        switch (cpt) {
+            case 1: hipLaunchKernelGGL((quantize_rows_reg_kernel<T, 1>), grid, block, 0, stream, x, width, ld, codes, scale, sum); break;
+            case 2: hipLaunchKernelGGL((quantize_rows_reg_kernel<T, 2>), grid, block, 0, stream, x, width, ld, codes, scale, sum); break;
+            case 3: hipLaunchKernelGGL((quantize_rows_reg_kernel<T, 3>), grid, block, 0, stream, x, width, ld, codes, scale, sum); break;
+            default: hipLaunchKernelGGL((quantize_rows_reg_kernel<T, 4>), grid, block, 0, stream, x, width, ld, codes, scale, sum); break;
+        }
+        return hipGetLastError();
+    }
     if (width % 16 == 0)
         return launch_vec<T, 16>(x, rows, width, ld, codes, scale, sum, aligned_for(16), stream);
     if (width % 8 == 0)

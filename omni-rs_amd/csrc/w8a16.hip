@@ -20,6 +20,8 @@
 //  * w8a16_mfma_kernel (prefill) converts each weight tile to f16 once while
 //    staging it into LDS, then runs v_mfma_f32_32x32x16_f16 on LDS fragments
 //    with the same swizzled, double-buffered layout as the W8A8 kernel.
+#include <cstdlib>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -51,14 +53,57 @@ __device__ __forceinline__ void i8x4_to_f16x4(u32 word, v2h& lo, v2h& hi) {
 // ---------------------------------------------------------------------------
 // Decode GEMV.
 // ---------------------------------------------------------------------------
-template <int MR, int CPL, int R>
+
+// Butterfly fold of N partial sums per lane across the 64 lanes of a wave:
+// at each offset O the lanes exchange half of their values, so N values cost
+// about N shuffles instead of 6N. Afterwards every lane holds one complete
+// sum, of index fold_index<N>(lane).
+template <int N, int O>
+struct Fold {
+    static __device__ __forceinline__ void run(float* v, int lane) {
+        if constexpr (O == 0) {
+            return;
+        } else if constexpr (N > 1) {
+            constexpr int H = N / 2;
+            const bool upper = (lane & O) != 0;
+#pragma unroll
+            for (int i = 0; i < H; ++i) {
+                const float send = upper ? v[i] : v[i + H];
+                const float keep = upper ? v[i + H] : v[i];
+                v[i] = keep + __shfl_xor(send, O, kWave);
+            }
+            Fold<H, O / 2>::run(v, lane);
+        } else {
+            v[0] += __shfl_xor(v[0], O, kWave);
+            Fold<1, O / 2>::run(v, lane);
+        }
+    }
+};
+
+template <int N>
+__device__ __forceinline__ int fold_index(int lane) {
+    int idx = 0;
+#pragma unroll
+    for (int l = 0, h = N / 2; h >= 1; ++l, h /= 2) idx += ((lane >> (5 - l)) & 1) * h;
+    return idx;
+}
+
+// MR activation rows (1, 2 or 4; unused rows are zero), CPL 16-element k
+// chunks per lane (the workgroup's 256 lanes own chunks tid + 256*j), R weight
+// rows per group. Weights of the next group are loaded while the current
+// group is reduced (PIPE).
+template <int MR, int CPL, int R, bool PIPE>
 __global__ __launch_bounds__(256) void w8a16_gemv_kernel(W8A16Args a) {
-    __shared__ float s_part[4][R * MR];
+    constexpr int V = R * MR;
+    static_assert((V & (V - 1)) == 0 && V <= 64, "power-of-two partial count");
+    __shared__ float s_part[4][V];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int64_t K = a.width;
-    const int64_t chunks = K / 16;  // 16 k elements per chunk
+    const int64_t chunks = K / 16;
+    const int64_t groups = (a.columns + R - 1) / R;
+    if ((int64_t)blockIdx.x >= groups) return;  // uniform across the block
 
     // Resident x: for each owned chunk j and row m, 16 halves as 8 f16 pairs.
     v2h xr[CPL][MR][8];
@@ -69,7 +114,7 @@ __global__ __launch_bounds__(256) void w8a16_gemv_kernel(W8A16Args a) {
         for (int m = 0; m < MR; ++m) {
             if (c < chunks && m < a.rows) {
                 const uint4* p = reinterpret_cast<const uint4*>(a.x + m * K + c * 16);
-                uint4 q0 = p[0], q1 = p[1];
+                const uint4 q0 = p[0], q1 = p[1];
                 xr[j][m][0] = bits_half2(q0.x); xr[j][m][1] = bits_half2(q0.y);
                 xr[j][m][2] = bits_half2(q0.z); xr[j][m][3] = bits_half2(q0.w);
                 xr[j][m][4] = bits_half2(q1.x); xr[j][m][5] = bits_half2(q1.y);
@@ -81,13 +126,11 @@ __global__ __launch_bounds__(256) void w8a16_gemv_kernel(W8A16Args a) {
         }
     }
 
-    const int64_t groups = (a.columns + R - 1) / R;
-    for (int64_t g = blockIdx.x; g < groups; g += gridDim.x) {
-        const int64_t n0 = g * R;
-        uint4 wv[R][CPL];
+    auto load = [&](uint4 (&wv)[R][CPL], int64_t g) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int64_t n = n0 + r < a.columns ? n0 + r : a.columns - 1;
+            const int64_t n0 = g * R + r;
+            const int64_t n = n0 < a.columns ? n0 : a.columns - 1;
             const int8_t* wrow = a.w + n * K;
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
@@ -96,56 +139,78 @@ __global__ __launch_bounds__(256) void w8a16_gemv_kernel(W8A16Args a) {
                                       : make_uint4(0, 0, 0, 0);
             }
         }
-        float part[R][MR];
+    };
+
+    uint4 cur[R][CPL];
+    load(cur, blockIdx.x);
+    for (int64_t g = blockIdx.x; g < groups; g += gridDim.x) {
+        uint4 nxt[R][CPL];
+        const int64_t gn = g + gridDim.x;
+        if constexpr (PIPE) {
+            if (gn < groups) load(nxt, gn);
+        }
+        float part[V];
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int m = 0; m < MR; ++m) part[r][m] = 0.0f;
+        for (int i = 0; i < V; ++i) part[i] = 0.0f;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
-                const u32 words[4] = {wv[r][j].x, wv[r][j].y, wv[r][j].z, wv[r][j].w};
+                const u32 words[4] = {cur[r][j].x, cur[r][j].y, cur[r][j].z, cur[r][j].w};
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     v2h w01, w23;
                     i8x4_to_f16x4(words[q], w01, w23);
 #pragma unroll
                     for (int m = 0; m < MR; ++m) {
-                        part[r][m] = __builtin_amdgcn_fdot2(w01, xr[j][m][2 * q], part[r][m], false);
-                        part[r][m] = __builtin_amdgcn_fdot2(w23, xr[j][m][2 * q + 1], part[r][m], false);
+                        float& p = part[r * MR + m];
+                        p = __builtin_amdgcn_fdot2(w01, xr[j][m][2 * q], p, false);
+                        p = __builtin_amdgcn_fdot2(w23, xr[j][m][2 * q + 1], p, false);
                     }
                 }
             }
         }
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                const float v = wave_sum_f32(part[r][m]);
-                if (lane == 0) s_part[wave][r * MR + m] = v;
-            }
+        Fold<V, 32>::run(part, lane);
+        if ((lane & (64 / V - 1)) == 0) s_part[wave][fold_index<V>(lane)] = part[0];
         __syncthreads();
-        if (tid < R * MR) {
+        if (tid < V) {
             const int r = tid / MR, m = tid % MR;
-            const int64_t n = n0 + r;
+            const int64_t n = g * R + r;
             if (n < a.columns && m < a.rows) {
-                float acc = s_part[0][tid] + s_part[1][tid] + s_part[2][tid] + s_part[3][tid];
+                const float acc = s_part[0][tid] + s_part[1][tid] + s_part[2][tid] + s_part[3][tid];
                 float v = acc * (float)a.scale[n];
                 if (a.bias) v += (float)a.bias[n];
                 a.out[(int64_t)m * a.columns + n] = (_Float16)v;
             }
         }
         __syncthreads();
+        if constexpr (PIPE) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) cur[r][j] = nxt[r][j];
+        } else {
+            if (gn < groups) load(cur, gn);
+        }
     }
 }
 
-template <int MR, int CPL, int R>
+// OMNI_W8A16_GRID=<n> pins the GEMV grid size (tuning aid; 0 = heuristic).
+int gemv_grid_override() {
+    static const int value = [] {
+        const char* v = std::getenv("OMNI_W8A16_GRID");
+        return v ? std::atoi(v) : 0;
+    }();
+    return value;
+}
+
+template <int MR, int CPL, int R, bool PIPE>
 hipError_t launch_gemv_cfg(const W8A16Args& a, hipStream_t stream) {
     const int64_t groups = (a.columns + R - 1) / R;
-    // Enough workgroups for several per CU; each loops over row groups.
-    const int64_t grid = groups < 2048 ? groups : 2048;
-    hipLaunchKernelGGL((w8a16_gemv_kernel<MR, CPL, R>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+    int64_t grid = gemv_grid_override() > 0 ? gemv_grid_override() : 1024;
+    if (grid > groups) grid = groups;
+    hipLaunchKernelGGL((w8a16_gemv_kernel<MR, CPL, R, PIPE>), dim3((unsigned)grid), dim3(256), 0,
+                       stream, a);
     return hipGetLastError();
 }
 
@@ -153,10 +218,10 @@ template <int MR>
 hipError_t launch_gemv_m(const W8A16Args& a, hipStream_t stream) {
     const int64_t cpl = (a.width / 16 + 255) / 256;
     switch (cpl) {
-        case 1: return launch_gemv_cfg<MR, 1, 8>(a, stream);
-        case 2: return launch_gemv_cfg<MR, 2, 4>(a, stream);
-        case 3: return launch_gemv_cfg<MR, 3, 4>(a, stream);
-        default: return launch_gemv_cfg<MR, 4, 4>(a, stream);
+        case 1: return launch_gemv_cfg<MR, 1, 8, true>(a, stream);
+        case 2: return launch_gemv_cfg<MR, 2, 4, true>(a, stream);
+        case 3: return launch_gemv_cfg<MR, 3, 4, MR < 4>(a, stream);
+        default: return launch_gemv_cfg<MR, 4, 4, MR < 4>(a, stream);
     }
 }
 
@@ -201,7 +266,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a16_mfma_kernel(W
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
     const int64_t K = a.width;
     const int ktiles = (int)((K + BK - 1) / BK);
-    auto swz = [](int r, int c) { return c ^ (r & 7); };
+    // 128-byte rows: two rows per 256-byte LDS window (see the W8A8 kernel).
+    auto swz = [](int r, int c) { return c ^ ((r >> 1) & 7); };
 
     uint4 ra[kALoads];
     uint4 rb[kBLoads];
@@ -326,8 +392,7 @@ hipError_t launch_w8a16_gemv(const W8A16Args& a, hipStream_t stream) {
     switch (a.rows) {
         case 1: return launch_gemv_m<1>(a, stream);
         case 2: return launch_gemv_m<2>(a, stream);
-        case 3: return launch_gemv_m<3>(a, stream);
-        default: return launch_gemv_m<4>(a, stream);
+        default: return launch_gemv_m<4>(a, stream);  // 3 rows run with one zero row
     }
 }
 

@@ -51,10 +51,7 @@ __device__ __forceinline__ void store_out(void* out, int64_t idx, float v, bool 
 // ---------------------------------------------------------------------------
 // Scalar lowering: one thread = one row x 4 consecutive columns, v_dot4 over K.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void w8a8_scalar_kernel(W8A8Args a) {
-    const int64_t col0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * 4;
-    const int64_t row = (int64_t)blockIdx.y * 4 + threadIdx.y;
-    if (row >= a.rows || col0 >= a.columns) return;
+__device__ __forceinline__ void w8a8_scalar_row(const W8A8Args& a, int64_t row, int64_t col0) {
     const int64_t words = a.width / 4;
     const u32* xr = reinterpret_cast<const u32*>(a.x + row * a.width);
     int acc[4] = {0, 0, 0, 0};
@@ -84,6 +81,14 @@ __global__ __launch_bounds__(256) void w8a8_scalar_kernel(W8A8Args a) {
     }
 }
 
+__global__ __launch_bounds__(256) void w8a8_scalar_kernel(W8A8Args a) {
+    const int64_t col0 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * 4;
+    if (col0 >= a.columns) return;
+    for (int64_t row = (int64_t)blockIdx.y * 4 + threadIdx.y; row < a.rows; row += (int64_t)gridDim.y * 4)
+        w8a8_scalar_row(a, row, col0);
+}
+
+
 // ---------------------------------------------------------------------------
 // MFMA lowering.
 // ---------------------------------------------------------------------------
@@ -98,7 +103,7 @@ __device__ __forceinline__ int xcd_remap(int b, int total) {
 }
 
 template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int GROUP_M>
-struct MfmaCfg {
+struct MfmaCfgUnused {
     static constexpr int kThreads = 64 * WAVES_M * WAVES_N;
     static constexpr int WM = BM / WAVES_M;
     static constexpr int WN = BN / WAVES_N;
@@ -110,170 +115,287 @@ struct MfmaCfg {
     static constexpr int kStageBytes = (BM + BN) * BK;
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile is a multiple of 32x32");
     static_assert(BK % 32 == 0 && kChunks <= 8, "K tile of 32..128 bytes");
-    static_assert((BM * kChunks) % kThreads == 0 && (BN * kChunks) % kThreads == 0,
-                  "loads divide evenly among threads");
+    // The last load slot of a thread may be idle when the tile's chunk count
+    // is not a multiple of the thread count.
+    static constexpr bool kAEven = (BM * kChunks) % kThreads == 0;
+    static constexpr bool kBEven = (BN * kChunks) % kThreads == 0;
 };
 
-// Physical 16-byte chunk slot of logical chunk c in tile row r.
+// Physical 16-byte chunk slot of logical chunk c in tile row r. gfx950 LDS
+// has 64 four-byte banks and serves ds_read_b128 / ds_write_b128 16 lanes at
+// a time, i.e. one 256-byte window: 256 / (16 * kChunks) consecutive rows
+// share a window, so the XOR key is the row's window index. A fragment read
+// (16 consecutive rows, one logical chunk) and a tile-row write (consecutive
+// chunks of consecutive rows) then touch 16 distinct 16-byte bank groups.
 template <int kChunks>
 __device__ __forceinline__ int swz(int r, int c) {
-    return c ^ (r & (kChunks - 1));
+    constexpr int kRowsPerWindow = 16 / kChunks;
+    return c ^ ((r / kRowsPerWindow) & (kChunks - 1));
 }
 
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int GROUP_M>
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a8_mfma_kernel(W8A8Args a) {
-    using C = MfmaCfg<BM, BN, BK, WAVES_M, WAVES_N, GROUP_M>;
+// Persistent int8-MFMA GEMM: 256 x BN output tiles (BN = 256, 192 or 128),
+// 4 waves in a 2 x 2 grid, each wave a 128 x BN/2 block of 32x32 int32
+// accumulators held in AGPRs; K tiles of 64 bytes.
+//
+// Every address is one per-thread base plus compile-time offsets: rows past
+// M (or N) are clamped to the last row, so loads need no predicates (their
+// accumulators are never stored); only a K tail (K % 64 != 0) zero-fills,
+// in a separate instantiation.
+//
+// Pipeline, per output tile:
+//  * K tiles t+1 .. t+PF are in flight in PF register sets while tile t is
+//    multiplied out of LDS (double-buffered LDS, one barrier per K tile);
+//  * after the last K tile, the workgroup's next output tile has its first PF
+//    K tiles issued before this tile's epilogue runs, so the epilogue's stores
+//    overlap the next tile's loads. The epilogue's per-row and per-column
+//    values are staged in LDS with the first K tile, so reading them never
+//    waits on the prefetch (vector loads complete in order).
+template <int BN, int PF, bool KTAIL, bool OUT16, bool DUMP>
+__global__ __launch_bounds__(256, 1) void w8a8_mfma_kernel(W8A8Args a) {
+    constexpr int BM = 256, BK = 64;
+    constexpr int WM = 128, WN = BN / 2;
+    constexpr int FM = WM / 32, FN = WN / 32;
+    constexpr int kALd = BM / 64;  // 16-byte loads per thread per K tile (A)
+    constexpr int kBLd = BN / 64;  // (W)
+    constexpr int kABuf = BM * BK, kBBuf = BN * BK;
+    static_assert(BN % 64 == 0 && WN % 32 == 0, "tile shape");
+
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    uint8_t* sA = smem;                    // [2][BM][BK]
-    uint8_t* sB = smem + 2 * BM * BK;      // [2][BN][BK]
+    uint8_t* sA = smem;                       // [2][BM][BK]
+    uint8_t* sB = smem + 2 * kABuf;           // [2][BN][BK]
+    float* sRowScale = reinterpret_cast<float*>(smem + 2 * (kABuf + kBBuf));  // [BM]
+    int* sRowSum = reinterpret_cast<int*>(sRowScale + BM);                    // [BM]
+    float* sColScale = reinterpret_cast<float*>(sRowSum + BM);                // [BN]
+    int* sColZero = reinterpret_cast<int*>(sColScale + BN);                   // [BN]
+    float* sColBias = reinterpret_cast<float*>(sColZero + BN);                // [BN]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wm = wave / WAVES_N;
-    const int wn = wave % WAVES_N;
-
-    // Tile coordinates: XCD-contiguous logical ids, then GROUP_M tile rows
-    // walked column by column so that concurrent tiles share A rows and W rows.
+    const int wm = wave >> 1, wn = wave & 1;
     const int tiles_m = (int)((a.rows + BM - 1) / BM);
     const int tiles_n = (int)((a.columns + BN - 1) / BN);
-    const int t = xcd_remap(blockIdx.x, tiles_m * tiles_n);
-    const int group_size = GROUP_M * tiles_n;
-    const int first_m = (t / group_size) * GROUP_M;
-    const int gm = min(tiles_m - first_m, GROUP_M);
-    const int tm = first_m + (t % group_size) % gm;
-    const int tn = (t % group_size) / gm;
-    const int64_t m0 = (int64_t)tm * BM;
-    const int64_t n0 = (int64_t)tn * BN;
-
-    const int64_t K = a.width;
-    const int ktiles = (int)((K + BK - 1) / BK);
-
-    // Global -> register staging for one K tile.
-    uint4 ra[C::kALoads];
-    uint4 rb[C::kBLoads];
-    auto load_tile = [&](int kt) {
-        const int64_t k0 = (int64_t)kt * BK;
-#pragma unroll
-        for (int i = 0; i < C::kALoads; ++i) {
-            const int id = tid + i * C::kThreads;
-            const int r = id / C::kChunks, c = id % C::kChunks;
-            const int64_t gr = m0 + r, gk = k0 + c * 16;
-            ra[i] = (gr < a.rows && gk < K)
-                        ? *reinterpret_cast<const uint4*>(a.x + gr * K + gk)
-                        : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < C::kBLoads; ++i) {
-            const int id = tid + i * C::kThreads;
-            const int r = id / C::kChunks, c = id % C::kChunks;
-            const int64_t gr = n0 + r, gk = k0 + c * 16;
-            rb[i] = (gr < a.columns && gk < K)
-                        ? *reinterpret_cast<const uint4*>(a.w + gr * K + gk)
-                        : make_uint4(0, 0, 0, 0);
-        }
-    };
-    auto store_tile = [&](int buf) {
-        uint8_t* dA = sA + buf * BM * BK;
-        uint8_t* dB = sB + buf * BN * BK;
-#pragma unroll
-        for (int i = 0; i < C::kALoads; ++i) {
-            const int id = tid + i * C::kThreads;
-            const int r = id / C::kChunks, c = id % C::kChunks;
-            *reinterpret_cast<uint4*>(dA + r * BK + swz<C::kChunks>(r, c) * 16) = ra[i];
-        }
-#pragma unroll
-        for (int i = 0; i < C::kBLoads; ++i) {
-            const int id = tid + i * C::kThreads;
-            const int r = id / C::kChunks, c = id % C::kChunks;
-            *reinterpret_cast<uint4*>(dB + r * BK + swz<C::kChunks>(r, c) * 16) = rb[i];
-        }
-    };
-
-    v16i acc[C::FM][C::FN];
-#pragma unroll
-    for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-        for (int j = 0; j < C::FN; ++j) acc[i][j] = v16i{};
-
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
-
-    const int frag_row = lane & 31;  // row of A (or of W) this lane feeds
-    const int frag_kc = lane >> 5;   // which 16-byte half of a 32-byte k step
-    for (int kt = 0; kt < ktiles; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < ktiles) load_tile(kt + 1);
-        const uint8_t* tA = sA + buf * BM * BK;
-        const uint8_t* tB = sB + buf * BN * BK;
-#pragma unroll
-        for (int ks = 0; ks < BK / 32; ++ks) {
-            const int c = ks * 2 + frag_kc;
-            v4i fa[C::FM], fb[C::FN];
-#pragma unroll
-            for (int i = 0; i < C::FM; ++i) {
-                const int r = wm * C::WM + i * 32 + frag_row;
-                fa[i] = *reinterpret_cast<const v4i*>(tA + r * BK + swz<C::kChunks>(r, c) * 16);
-            }
-#pragma unroll
-            for (int j = 0; j < C::FN; ++j) {
-                const int r = wn * C::WN + j * 32 + frag_row;
-                fb[j] = *reinterpret_cast<const v4i*>(tB + r * BK + swz<C::kChunks>(r, c) * 16);
-            }
-#pragma unroll
-            for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-                for (int j = 0; j < C::FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
-        }
-        if (kt + 1 < ktiles) store_tile(buf ^ 1);
-        __syncthreads();
-    }
-
-    // Epilogue straight from the accumulators. 32x32 accumulator layout:
-    // lane holds column (lane & 31) and rows 8*(r/4) + 4*(lane/32) + (r%4).
+    const int total = tiles_m * tiles_n;
+    const int K = (int)a.width;
+    const int ktiles = (K + BK - 1) / BK;
     const bool has_bias = a.bias != nullptr;
+    const bool has_zero = a.w_zero != nullptr;
+    constexpr int kGroupM = 4;
+
+    // Global->LDS copy slot of this thread: tile row ld_row + 64*i, chunk ld_c.
+    const int ld_row = tid >> 2, ld_c = tid & 3;
+    // Swizzled LDS offset of that slot (the XOR key (row / 4) % 4 does not
+    // depend on i, since 64*i is a multiple of 16 rows).
+    const int st_off = ld_row * BK + ((ld_c ^ ((ld_row >> 2) & 3)) << 4);
+    // Fragment read bases for k steps 0 and 1 (32 bytes each): lane feeds row
+    // (lane & 31), 16-byte half (lane >> 5).
+    const int fr = lane & 31, fh = lane >> 5, fq = (fr >> 2) & 3;
+    const int fragA0 = (wm * WM + fr) * BK + (((0 + fh) ^ fq) << 4);
+    const int fragA1 = (wm * WM + fr) * BK + (((2 + fh) ^ fq) << 4);
+    const int fragB0 = (wn * WN + fr) * BK + (((0 + fh) ^ fq) << 4);
+    const int fragB1 = (wn * WN + fr) * BK + (((2 + fh) ^ fq) << 4);
+
+    int L = xcd_remap(blockIdx.x, gridDim.x);
+    if (L >= total) return;
+
+    int64_t m0 = 0, n0 = 0;
+    const uint8_t* gA;  // this thread's A row for slot 0, chunk ld_c, k = 0
+    const uint8_t* gB;
+    int offA[kALd], offB[kBLd];  // byte offsets of slots i > 0 from gA / gB
+    auto setup_tile = [&](int l) {
+        const int group_size = kGroupM * tiles_n;
+        const int first_m = (l / group_size) * kGroupM;
+        const int gm = min(tiles_m - first_m, kGroupM);
+        // Integer division runs on the VALU; pin the (uniform) results to SGPRs.
+        m0 = (int64_t)__builtin_amdgcn_readfirstlane(first_m + (l % group_size) % gm) * BM;
+        n0 = (int64_t)__builtin_amdgcn_readfirstlane((l % group_size) / gm) * BN;
+        const int64_t last_r = a.rows - 1, last_c = a.columns - 1;
+        const int64_t r0 = min(m0 + ld_row, last_r);
+        const int64_t c0 = min(n0 + ld_row, last_c);
+        gA = a.x + r0 * K + ld_c * 16;
+        gB = a.w + c0 * K + ld_c * 16;
 #pragma unroll
-    for (int j = 0; j < C::FN; ++j) {
-        const int64_t col = n0 + wn * C::WN + j * 32 + (lane & 31);
-        if (col >= a.columns) continue;
-        const float ws = a.w_scale[col];
-        const int zero = a.w_zero ? a.w_zero[col] : 0;
-        const float bias = has_bias ? a.bias[col] : 0.0f;
+        for (int i = 0; i < kALd; ++i) offA[i] = (int)((min(m0 + ld_row + 64 * i, last_r) - r0) * K);
 #pragma unroll
-        for (int i = 0; i < C::FM; ++i) {
+        for (int i = 0; i < kBLd; ++i) offB[i] = (int)((min(n0 + ld_row + 64 * i, last_c) - c0) * K);
+    };
+
+    uint4 ra[PF][kALd];
+    uint4 rb[PF][kBLd];
+    auto load_tile = [&](int kt, uint4 (&xa)[kALd], uint4 (&xb)[kBLd]) {
+        const int k0 = kt * BK;
+        const bool in_k = !KTAIL || k0 + ld_c * 16 < K;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + wm * C::WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (row >= a.rows) continue;
-                const int64_t idx = row * a.columns + col;
-                const int v = acc[i][j][r];
-                if (a.acc_dump) a.acc_dump[idx] = v;
-                const int sum = a.w_zero ? a.x_sum[row] : 0;
-                store_out(a.out, idx, w8a8_epilogue(v, sum, zero, a.x_scale[row], ws, bias, has_bias),
-                          a.out_f16);
+        for (int i = 0; i < kALd; ++i)
+            xa[i] = in_k ? *reinterpret_cast<const uint4*>(gA + offA[i] + k0) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < kBLd; ++i)
+            xb[i] = in_k ? *reinterpret_cast<const uint4*>(gB + offB[i] + k0) : make_uint4(0, 0, 0, 0);
+    };
+    auto store_tile = [&](int buf, const uint4 (&xa)[kALd], const uint4 (&xb)[kBLd]) {
+        uint8_t* dA = sA + buf * kABuf + st_off;
+        uint8_t* dB = sB + buf * kBBuf + st_off;
+#pragma unroll
+        for (int i = 0; i < kALd; ++i) *reinterpret_cast<uint4*>(dA + i * 64 * BK) = xa[i];
+#pragma unroll
+        for (int i = 0; i < kBLd; ++i) *reinterpret_cast<uint4*>(dB + i * 64 * BK) = xb[i];
+    };
+    // Epilogue values of a tile: thread tid holds row tid's and column tid's.
+    float p_rs = 0.0f, p_cs = 0.0f, p_cb = 0.0f;
+    int p_rsum = 0, p_cz = 0;
+    auto load_params = [&]() {
+        const int64_t row = min(m0 + tid, (int64_t)a.rows - 1);
+        p_rs = a.x_scale[row];
+        p_rsum = has_zero ? a.x_sum[row] : 0;
+        if (tid < BN) {
+            const int64_t col = min(n0 + tid, (int64_t)a.columns - 1);
+            p_cs = a.w_scale[col];
+            p_cz = has_zero ? a.w_zero[col] : 0;
+            p_cb = has_bias ? a.bias[col] : 0.0f;
+        }
+    };
+    auto store_params = [&]() {
+        sRowScale[tid] = p_rs;
+        sRowSum[tid] = p_rsum;
+        if (tid < BN) {
+            sColScale[tid] = p_cs;
+            sColZero[tid] = p_cz;
+            sColBias[tid] = p_cb;
+        }
+    };
+    // Every prefetch is issued unconditionally, clamped to the last K tile,
+    // so that all paths through the K loop carry the same sequence of loads:
+    // vector loads complete in order, and the compiler can then wait for just
+    // the oldest register set instead of all outstanding loads.
+    auto issue_tile_start = [&]() {
+        load_params();
+#pragma unroll
+        for (int u = 0; u < PF; ++u) load_tile(min(u, ktiles - 1), ra[u], rb[u]);
+    };
+
+    setup_tile(L);
+    issue_tile_start();
+
+    while (true) {
+        v16i acc[FM][FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
+
+        __syncthreads();  // the previous tile's epilogue is done with LDS
+        store_params();
+        store_tile(0, ra[0], rb[0]);
+        __syncthreads();
+        load_tile(min(PF, ktiles - 1), ra[0], rb[0]);
+
+        for (int t0 = 0; t0 < ktiles; t0 += PF) {
+#pragma unroll
+            for (int u = 0; u < PF; ++u) {
+                const int kt = t0 + u;
+                const int buf = kt & 1;
+                if (kt < ktiles) {
+                    const uint8_t* tA = sA + buf * kABuf;
+                    const uint8_t* tB = sB + buf * kBBuf;
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) {
+                        v4i fa[FM], fb[FN];
+                        const uint8_t* pa = tA + (ks ? fragA1 : fragA0);
+                        const uint8_t* pb = tB + (ks ? fragB1 : fragB0);
+#pragma unroll
+                        for (int i = 0; i < FM; ++i) fa[i] = *reinterpret_cast<const v4i*>(pa + i * 32 * BK);
+#pragma unroll
+                        for (int j = 0; j < FN; ++j) fb[j] = *reinterpret_cast<const v4i*>(pb + j * 32 * BK);
+#pragma unroll
+                        for (int i = 0; i < FM; ++i)
+#pragma unroll
+                            for (int j = 0; j < FN; ++j)
+                                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                    }
+                }
+                // Tile kt+1 lives in register set (u+1) % PF; stage it, then
+                // reuse the set for tile kt+1+PF.
+                const int next = (u + 1) % PF;  // a constant once u is unrolled
+                if (kt + 1 < ktiles) store_tile(buf ^ 1, ra[next], rb[next]);
+                __syncthreads();
+                load_tile(min(kt + 1 + PF, ktiles - 1), ra[next], rb[next]);
             }
         }
+
+        // Issue the next tile's first K tiles, then run this tile's epilogue.
+        const int64_t em0 = m0, en0 = n0;
+        const int Ln = L + gridDim.x;
+        const bool more = Ln < total;
+        if (more) {
+            setup_tile(Ln);
+            issue_tile_start();
+        }
+
+        // 32x32 accumulator layout: lane holds column (lane & 31) and rows
+        // 8*(r/4) + 4*(lane/32) + (r%4) of each 32x32 block. Offsets are
+        // 32-bit, relative to the tile's first element (the host guarantees
+        // 256 * columns < 2^31).
+        const int N = (int)a.columns;
+        const int64_t tile_base = em0 * a.columns + en0;
+        // Keep the epilogue's lane-dependent index math inside the tile loop:
+        // hoisted out of it, its values would stay live across the K loop.
+        int efr = fr, efh = fh;
+        asm volatile("" : "+v"(efr), "+v"(efh));
+        const bool full = em0 + BM <= a.rows && en0 + BN <= a.columns;
+        const int rows_left = (int)min((int64_t)BM, a.rows - em0);
+        const int cols_left = (int)min((int64_t)BN, a.columns - en0);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int lr0 = wm * WM + i * 32 + 4 * efh;
+                const int lc = wn * WN + j * 32 + efr;
+                const float ws = sColScale[lc];
+                const int zero = sColZero[lc];
+                const float bias = sColBias[lc];
+                const int base = lr0 * N + lc;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 s4 = *reinterpret_cast<const float4*>(sRowScale + lr0 + 8 * q);
+                    const int4 z4 = *reinterpret_cast<const int4*>(sRowSum + lr0 + 8 * q);
+                    const float rs[4] = {s4.x, s4.y, s4.z, s4.w};
+                    const int rsum[4] = {z4.x, z4.y, z4.z, z4.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int r = 4 * q + e;
+                        const int dr = 8 * q + e;
+                        const int off = base + dr * N;
+                        const int v = acc[i][j][r];
+                        const float o = w8a8_epilogue(v, rsum[e], zero, rs[e], ws, bias, has_bias);
+                        if (full || (lr0 + dr < rows_left && lc < cols_left)) {
+                            if constexpr (DUMP) a.acc_dump[tile_base + off] = v;
+                            if constexpr (OUT16)
+                                static_cast<_Float16*>(a.out)[tile_base + off] = (_Float16)o;
+                            else
+                                static_cast<float*>(a.out)[tile_base + off] = o;
+                        }
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        if (!more) break;
+        L = Ln;
     }
 }
 
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int GROUP_M>
-hipError_t launch_cfg(const W8A8Args& a, hipStream_t stream) {
-    using C = MfmaCfg<BM, BN, BK, WAVES_M, WAVES_N, GROUP_M>;
-    auto kernel = w8a8_mfma_kernel<BM, BN, BK, WAVES_M, WAVES_N, GROUP_M>;
-    const size_t smem = 2 * (size_t)C::kStageBytes;
-    // Dynamic LDS above 64 KiB needs an opt-in; setting it is idempotent.
-    static std::atomic<bool> configured{false};
-    if (!configured.load(std::memory_order_acquire)) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-        if (e != hipSuccess) return e;
-        configured.store(true, std::memory_order_release);
+// Compute units of the current device (cached per device).
+int num_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        cached[dev] = n;
     }
-    const int64_t tiles = ((a.rows + BM - 1) / BM) * ((a.columns + BN - 1) / BN);
-    hipLaunchKernelGGL(kernel, dim3((unsigned)tiles), dim3(C::kThreads), smem, stream, a);
-    return hipGetLastError();
+    return cached[dev];
 }
 
 // OMNI_W8A8_TILE=<n> pins one tile configuration (tuning aid; 0 = heuristic).
@@ -285,12 +407,49 @@ int w8a8_tile_override() {
     return value;
 }
 
+template <int BN, int PF, bool KTAIL, bool OUT16, bool DUMP>
+hipError_t launch_cfg(const W8A8Args& a, hipStream_t stream) {
+    auto kernel = w8a8_mfma_kernel<BN, PF, KTAIL, OUT16, DUMP>;
+    const size_t smem = 2 * (size_t)(256 + BN) * 64 + (size_t)(2 * 256 + 3 * BN) * 4;
+    // Dynamic LDS above 64 KiB needs an opt-in; setting it is idempotent.
+    static std::atomic<bool> configured{false};
+    if (!configured.load(std::memory_order_acquire)) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+        if (e != hipSuccess) return e;
+        configured.store(true, std::memory_order_release);
+    }
+    const int64_t tiles = ((a.rows + 255) / 256) * ((a.columns + BN - 1) / BN);
+    // One persistent workgroup per CU (the kernel's occupancy is one), each
+    // looping over tiles.
+    const int64_t grid = tiles < num_cus() ? tiles : num_cus();
+    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(256), smem, stream, a);
+    return hipGetLastError();
+}
+
+template <int BN, int PF, bool OUT16, bool DUMP>
+hipError_t launch_out(const W8A8Args& a, hipStream_t stream) {
+    if (a.width % 64 != 0) return launch_cfg<BN, PF, true, OUT16, DUMP>(a, stream);
+    return launch_cfg<BN, PF, false, OUT16, DUMP>(a, stream);
+}
+
+template <int BN, int PF>
+hipError_t launch_bn(const W8A8Args& a, hipStream_t stream) {
+    if (a.acc_dump) {
+        if (a.out_f16) return launch_out<BN, PF, true, true>(a, stream);
+        return launch_out<BN, PF, false, true>(a, stream);
+    }
+    if (a.out_f16) return launch_out<BN, PF, true, false>(a, stream);
+    return launch_out<BN, PF, false, false>(a, stream);
+}
+
 }  // namespace
 
 hipError_t launch_w8a8_scalar(const W8A8Args& a, hipStream_t stream) {
     if (a.rows == 0 || a.columns == 0) return hipSuccess;
     dim3 block(64, 4);
-    dim3 grid((unsigned)((a.columns + 255) / 256), (unsigned)((a.rows + 3) / 4));
+    const int64_t row_blocks = (a.rows + 3) / 4;
+    dim3 grid((unsigned)((a.columns + 255) / 256), (unsigned)(row_blocks < 65535 ? row_blocks : 65535));
     hipLaunchKernelGGL(w8a8_scalar_kernel, grid, block, 0, stream, a);
     return hipGetLastError();
 }
@@ -298,15 +457,25 @@ hipError_t launch_w8a8_scalar(const W8A8Args& a, hipStream_t stream) {
 hipError_t launch_w8a8_mfma(const W8A8Args& a, hipStream_t stream) {
     if (a.rows == 0 || a.columns == 0) return hipSuccess;
     switch (w8a8_tile_override()) {
-        case 1: return launch_cfg<256, 256, 64, 2, 2, 4>(a, stream);
-        case 2: return launch_cfg<256, 256, 128, 2, 4, 4>(a, stream);
-        case 3: return launch_cfg<256, 256, 64, 2, 4, 4>(a, stream);
-        case 4: return launch_cfg<256, 128, 128, 2, 2, 4>(a, stream);
-        case 5: return launch_cfg<128, 128, 128, 2, 2, 4>(a, stream);
-        case 6: return launch_cfg<256, 128, 64, 2, 2, 4>(a, stream);
+        case 1: return launch_bn<256, 1>(a, stream);
+        case 2: return launch_bn<256, 2>(a, stream);
+        case 3: return launch_bn<192, 2>(a, stream);
+        case 4: return launch_bn<128, 2>(a, stream);
+        case 5: return launch_bn<192, 1>(a, stream);
         default: break;
     }
-    return launch_cfg<256, 256, 64, 2, 4, 4>(a, stream);
+    // Column tile: the one whose tiles fill the CUs best (useful work over the
+    // work of the rounds of tiles launched), wider on ties. 256-wide tiles
+    // need every AGPR for accumulators and are kept for the override only.
+    const int64_t cus = num_cus();
+    const int64_t tm = (a.rows + 255) / 256;
+    auto fill = [&](int64_t bn) {  // columns / (launched tile rounds x cus x bn) per tile row
+        const int64_t tn = (a.columns + bn - 1) / bn;
+        const int64_t rounds = (tm * tn + cus - 1) / cus;
+        return (double)a.columns * (double)tm / ((double)rounds * (double)cus * (double)bn);
+    };
+    if (fill(192) >= fill(128) * 0.97) return launch_bn<192, 2>(a, stream);
+    return launch_bn<128, 2>(a, stream);
 }
 
 }  // namespace omni

@@ -76,6 +76,25 @@ def test_quantize_rows_ties_and_strided_input(oracle):
     assert np.array_equal(host(codes), ocodes) and np.array_equal(host(total), ototal)
 
 
+def test_quantize_rows_near_ties_at_random_scales(oracle):
+    # Quotients within a few ulps of k + 0.5 at row scales from 2^-107 to 2^33:
+    # the division must be correctly rounded for every code to match.
+    rng = np.random.default_rng(11)
+    rows, width = 512, 256
+    peaks = np.ldexp(1.0 + rng.random(rows), rng.integers(-100, 40, rows)).astype(np.float32)
+    s = np.maximum(peaks / np.float32(127), np.float32(1e-30)).astype(np.float32)
+    k = rng.integers(0, 127, (rows, width))
+    h = ((k + 0.5) * s[:, None].astype(np.float64)).astype(np.float32)
+    h = (h.view(np.int32) + rng.integers(-4, 5, (rows, width)).astype(np.int32)).view(np.float32)
+    x = np.minimum(h, peaks[:, None]) * np.where(rng.random((rows, width)) < 0.5, -1, 1).astype(np.float32)
+    x[:, 0] = peaks
+    codes, rs, total = oi.quantize_rows(dev(x))
+    ocodes, ors, ototal = oracle.quantize_rows(x)
+    assert np.array_equal(host(rs).view(np.uint32), ors.view(np.uint32))
+    assert np.array_equal(host(codes), ocodes)
+    assert np.array_equal(host(total), ototal)
+
+
 # -- the reference's own tests ------------------------------------------------------
 
 
