@@ -19,6 +19,8 @@
 // (Markstein's correction step), which returns RN(x / s) whenever the
 // residual r is exact; rows with s < 2^-90 (where r can leave the normal
 // range) use the hardware-expanded IEEE division instead.
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -59,23 +61,36 @@ __device__ __forceinline__ void load_row_chunk(const T* __restrict__ p, float (&
 
 
 // RN(x / s) given y = RN(1 / s); see the file comment for when it is exact.
-__device__ __forceinline__ float div_rn(float x, float s, float y, bool tiny_scale) {
+template <bool TINY>
+__device__ __forceinline__ float div_rn(float x, float s, float y) {
 #pragma clang fp contract(off)
-    if (tiny_scale) return x / s;
+    if constexpr (TINY) return x / s;
     const float q0 = x * y;
     const float r = __builtin_fmaf(-q0, s, x);
     return __builtin_fmaf(r, y, q0);
 }
 
-// Codes of four consecutive values packed little-endian into one word.
-__device__ __forceinline__ u32 pack4(const float* v, float s, float y, bool tiny, int& sum) {
-    u32 word = 0;
+// Codes of four consecutive values packed little-endian into one word; the
+// codes' sum is accumulated with one v_dot4 against 1,1,1,1.
+//
+// Rounding: trunc(q + copysign(0.5, q)) equals sign(q) * floor(|q| + 0.5)
+// with the same f32 addition as the reference (q - 0.5 is exactly
+// -(|q| + 0.5)), and v_cvt_i32_f32 truncates toward zero and maps NaN to 0.
+// |q| <= 127 * (1 + 2^-23) always (the row scale is the peak / 127), so the
+// clamp to [-128, 127] only ever matters for NaN/Inf-derived values.
+template <bool TINY>
+__device__ __forceinline__ u32 pack4(const float* v, float s, float y, int& sum) {
+    int c[4];
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-        const int q = quantize_code(div_rn(v[b], s, y, tiny));
-        sum += q;
-        word |= (u32)(q & 255) << (8 * b);
+        const float q = div_rn<TINY>(v[b], s, y);
+        const int r = (int)(q + __builtin_copysignf(0.5f, q));
+        c[b] = r < -128 ? -128 : (r > 127 ? 127 : r);
     }
+    const u32 lo = __builtin_amdgcn_perm((u32)c[1], (u32)c[0], 0x0c0c0400u);  // c0.b0, c1.b0
+    const u32 hi = __builtin_amdgcn_perm((u32)c[3], (u32)c[2], 0x0c0c0400u);  // c2.b0, c3.b0
+    const u32 word = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+    sum = __builtin_amdgcn_sdot4((int)word, 0x01010101, sum, false);
     return word;
 }
 
@@ -125,18 +140,22 @@ __global__ __launch_bounds__(256) void quantize_rows_reg_kernel(
     const bool tiny = s < 0x1p-90f;
     int local = 0;
     uint8_t* dst = codes + row * width;
+    auto emit = [&](auto tiny_tag) {
+        constexpr bool kTiny = decltype(tiny_tag)::value;
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-        const int c = tid + 256 * j;
-        if (c < chunks) {
-            uint4 w;
-            w.x = pack4(&v[j][0], s, y, tiny, local);
-            w.y = pack4(&v[j][4], s, y, tiny, local);
-            w.z = pack4(&v[j][8], s, y, tiny, local);
-            w.w = pack4(&v[j][12], s, y, tiny, local);
-            *reinterpret_cast<uint4*>(dst + (int64_t)c * 16) = w;
+        for (int j = 0; j < CPT; ++j) {
+            const int c = tid + 256 * j;
+            if (c < chunks) {
+                uint4 w;
+                w.x = pack4<kTiny>(&v[j][0], s, y, local);
+                w.y = pack4<kTiny>(&v[j][4], s, y, local);
+                w.z = pack4<kTiny>(&v[j][8], s, y, local);
+                w.w = pack4<kTiny>(&v[j][12], s, y, local);
+                *reinterpret_cast<uint4*>(dst + (int64_t)c * 16) = w;
+            }
         }
-    }
+    };
+    if (tiny) emit(std::true_type{}); else emit(std::false_type{});
     if (sum_out) {
         local = wave_sum_i32(local);
         if ((tid & 63) == 0) s_sum[tid >> 6] = local;
@@ -191,20 +210,24 @@ __global__ __launch_bounds__(256) void quantize_rows_wave_kernel(
     const bool tiny = s < 0x1p-90f;
     int local = 0;
     uint8_t* dst = codes + row * width;
+    auto emit = [&](auto tiny_tag) {
+        constexpr bool kTiny = decltype(tiny_tag)::value;
 #pragma unroll
-    for (int j = 0; j < CPW; ++j) {
-        const int c = lane + 64 * j;
-        if (c < chunks) {
-            float v[16];
-            unpack(j, v);
-            uint4 w;
-            w.x = pack4(&v[0], s, y, tiny, local);
-            w.y = pack4(&v[4], s, y, tiny, local);
-            w.z = pack4(&v[8], s, y, tiny, local);
-            w.w = pack4(&v[12], s, y, tiny, local);
-            *reinterpret_cast<uint4*>(dst + (int64_t)c * 16) = w;
+        for (int j = 0; j < CPW; ++j) {
+            const int c = lane + 64 * j;
+            if (c < chunks) {
+                float v[16];
+                unpack(j, v);
+                uint4 w;
+                w.x = pack4<kTiny>(&v[0], s, y, local);
+                w.y = pack4<kTiny>(&v[4], s, y, local);
+                w.z = pack4<kTiny>(&v[8], s, y, local);
+                w.w = pack4<kTiny>(&v[12], s, y, local);
+                *reinterpret_cast<uint4*>(dst + (int64_t)c * 16) = w;
+            }
         }
-    }
+    };
+    if (tiny) emit(std::true_type{}); else emit(std::false_type{});
     if (sum_out) {
         local = wave_sum_i32(local);
         if (lane == 0) sum_out[row] = local;
@@ -243,8 +266,13 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
         float v[VEC];
         load_row_chunk<T, VEC, ALIGNED>(src + c * VEC, v);
         u32 words[VEC / 4];
+        if (tiny) {
 #pragma unroll
-        for (int w = 0; w < VEC / 4; ++w) words[w] = pack4(&v[4 * w], row_scale, y, tiny, local);
+            for (int w = 0; w < VEC / 4; ++w) words[w] = pack4<true>(&v[4 * w], row_scale, y, local);
+        } else {
+#pragma unroll
+            for (int w = 0; w < VEC / 4; ++w) words[w] = pack4<false>(&v[4 * w], row_scale, y, local);
+        }
         if constexpr (ALIGNED && VEC == 16) {
             *reinterpret_cast<uint4*>(dst + c * VEC) = make_uint4(words[0], words[1], words[2], words[3]);
         } else if constexpr (ALIGNED && VEC == 8) {
@@ -289,7 +317,7 @@ hipError_t launch_typed(const T* x, int64_t rows, int64_t width, int64_t ld, uin
         return base % align == 0 && (ld * (int64_t)sizeof(T)) % align == 0 && cbase % vec == 0;
     };
     // One wave per row while the row fits in registers (16 KiB of input).
-    constexpr int64_t kWaveMax = 8192 / (int64_t)sizeof(T) * 2;  // 16384 f16, 8192 f32
+    constexpr int64_t kWaveMax = 32768 / (int64_t)sizeof(T);  // 32 KiB of input: 16384 f16, 8192 f32
     if (width % 16 == 0 && width <= kWaveMax && aligned_for(16)) {
         const int cpw = (int)((width / 16 + 63) / 64);
         dim3 grid((unsigned)((rows + 3) / 4)), block(256);

@@ -103,7 +103,6 @@ __global__ __launch_bounds__(256) void w8a16_gemv_kernel(W8A16Args a) {
     const int64_t K = a.width;
     const int64_t chunks = K / 16;
     const int64_t groups = (a.columns + R - 1) / R;
-    if ((int64_t)blockIdx.x >= groups) return;  // uniform across the block
 
     // Resident x: for each owned chunk j and row m, 16 halves as 8 f16 pairs.
     v2h xr[CPL][MR][8];
@@ -134,21 +133,29 @@ __global__ __launch_bounds__(256) void w8a16_gemv_kernel(W8A16Args a) {
             const int8_t* wrow = a.w + n * K;
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
-                const int64_t c = tid + 256 * j;
-                wv[r][j] = c < chunks ? *reinterpret_cast<const uint4*>(wrow + c * 16)
-                                      : make_uint4(0, 0, 0, 0);
+                // Clamped, not predicated: a predicated load lets the compiler
+                // pull its consumers next to it, which waits for it at once.
+                // Chunks past K meet zero activations, so their value is moot.
+                const int64_t c = tid + 256 * j < chunks ? tid + 256 * j : chunks - 1;
+                wv[r][j] = *reinterpret_cast<const uint4*>(wrow + c * 16);
             }
         }
     };
 
-    uint4 cur[R][CPL];
-    load(cur, blockIdx.x);
-    for (int64_t g = blockIdx.x; g < groups; g += gridDim.x) {
-        uint4 nxt[R][CPL];
-        const int64_t gn = g + gridDim.x;
-        if constexpr (PIPE) {
-            if (gn < groups) load(nxt, gn);
-        }
+    // Row groups blockIdx.x, blockIdx.x + gridDim.x, ... (measured faster on
+    // MI355X than giving each workgroup a contiguous range).
+    const int64_t g_begin = blockIdx.x, g_end = groups, g_step = gridDim.x;
+    // One row group: wait for its weights (cur), issue the next group's
+    // (nxt, unconditional: the last group re-reads itself from L2, so every
+    // path issues the same loads and the wait for cur leaves nxt in flight),
+    // then dot, reduce and store. The loop below alternates two register sets.
+    auto group = [&](uint4 (&cur)[R][CPL], uint4 (&nxt)[R][CPL], int64_t g) {
+        // This group's scale and bias, loaded by every thread (row tid % R)
+        // ahead of the next group's weights.
+        const int64_t n_ep = min(g * R + (tid / MR) % R, a.columns - 1);
+        const _Float16 sc_h = a.scale[n_ep];
+        const _Float16 bi_h = (a.bias ? a.bias : a.scale)[n_ep];  // unconditional load
+        if constexpr (PIPE) load(nxt, g + g_step < g_end ? g + g_step : g);
         float part[V];
 #pragma unroll
         for (int i = 0; i < V; ++i) part[i] = 0.0f;
@@ -178,19 +185,25 @@ __global__ __launch_bounds__(256) void w8a16_gemv_kernel(W8A16Args a) {
             const int64_t n = g * R + r;
             if (n < a.columns && m < a.rows) {
                 const float acc = s_part[0][tid] + s_part[1][tid] + s_part[2][tid] + s_part[3][tid];
-                float v = acc * (float)a.scale[n];
-                if (a.bias) v += (float)a.bias[n];
-                a.out[(int64_t)m * a.columns + n] = (_Float16)v;
+                const float bi = a.bias ? (float)bi_h : 0.0f;
+                a.out[(int64_t)m * a.columns + n] = (_Float16)(acc * (float)sc_h + bi);
             }
         }
         __syncthreads();
+        if constexpr (!PIPE) {
+            if (g + g_step < g_end) load(cur, g + g_step);
+        }
+    };
+
+    uint4 wa[R][CPL], wb[R][CPL];
+    load(wa, g_begin);
+    for (int64_t g = g_begin; g < g_end; g += 2 * g_step) {
         if constexpr (PIPE) {
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-#pragma unroll
-                for (int j = 0; j < CPL; ++j) cur[r][j] = nxt[r][j];
+            group(wa, wb, g);
+            if (g + g_step < g_end) group(wb, wa, g + g_step);
         } else {
-            if (gn < groups) load(cur, gn);
+            group(wa, wa, g);
+            if (g + g_step < g_end) group(wa, wa, g + g_step);
         }
     }
 }
@@ -207,7 +220,12 @@ int gemv_grid_override() {
 template <int MR, int CPL, int R, bool PIPE>
 hipError_t launch_gemv_cfg(const W8A16Args& a, hipStream_t stream) {
     const int64_t groups = (a.columns + R - 1) / R;
-    int64_t grid = gemv_grid_override() > 0 ? gemv_grid_override() : 1024;
+    // Up to 1024 workgroups (4 per CU), but at least two row groups per
+    // workgroup where there are enough, so that the next group's weights
+    // stream in while the current one is reduced (256-1024, measured).
+    int64_t grid = (groups + 1) / 2;
+    grid = grid < 256 ? 256 : (grid > 1024 ? 1024 : grid);
+    if (gemv_grid_override() > 0) grid = gemv_grid_override();
     if (grid > groups) grid = groups;
     hipLaunchKernelGGL((w8a16_gemv_kernel<MR, CPL, R, PIPE>), dim3((unsigned)grid), dim3(256), 0,
                        stream, a);

@@ -384,6 +384,231 @@ __global__ __launch_bounds__(256, 1) void w8a8_mfma_kernel(W8A8Args a) {
     }
 }
 
+// LDS-DMA GEMM (K % 64 == 0): one 256 x BN output tile per workgroup, two
+// workgroups per CU so that one's epilogue and pipeline ramp overlap the
+// other's K loop. K tiles are copied global -> LDS by global_load_lds_dwordx4:
+// no staging registers and no LDS write instructions. A wave's copy
+// instruction fills a contiguous 1 KiB block (16 tile rows of 64 bytes, lane
+// l at byte 16*l), so the bank swizzle is applied on the global side: lane l
+// reads logical chunk (l % 4) ^ ((l / 16) % 4) of row l / 4 of the block. The
+// S stage buffers are distinct LDS arrays and the K loop is unrolled by S
+// (S divides the K-tile count) so every copy and read names its array
+// statically; the wait for K tile kt is vmcnt(copies issued after it),
+// leaving S-2 later tiles in flight, then one barrier per K tile.
+#define OMNI_LDS __attribute__((address_space(3)))
+
+// One 16-byte-per-lane global -> LDS copy (global_load_lds_dwordx4). The
+// builtin needs a gfx950 target feature that the host compilation pass lacks,
+// so it is emitted in the device pass only.
+__device__ __forceinline__ void lds_copy16(const uint8_t* src, uint8_t* lds_dst) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_global_load_lds(src, (OMNI_LDS void*)lds_dst, 16, 0, 0);
+#endif
+}
+
+template <int BN, int WAVES_M>
+struct DmaCfg {
+    static constexpr int BM = 128 * WAVES_M, BK = 64;
+    static constexpr int kWaves = 2 * WAVES_M;
+    static constexpr int kStageBytes = (BM + BN) * BK;
+    // 1 KiB copies (16 rows) per K tile: A's are spread over all waves; W's
+    // over the first 4 waves (BN / 64 each).
+    static constexpr int kACopies = BM / 16 / kWaves;
+    static constexpr int kBCopies = BN / 64;
+    static_assert(BM % (16 * kWaves) == 0, "A copies divide among waves");
+};
+
+// s_waitcnt vmcnt(N) (and lgkmcnt(0) when LGKM0) for a compile-time N.
+template <int N, bool LGKM0 = false>
+__device__ __forceinline__ void s_waitcnt_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    // gfx9 encoding: vmcnt[3:0] | expcnt << 4 | lgkmcnt << 8 | vmcnt[5:4] << 14
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((LGKM0 ? 0 : 15) << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier for the LDS-DMA pipeline. __syncthreads() would wait for
+// every outstanding vector-memory operation (its release fence counts the
+// in-flight global->LDS copies as LDS writes); here the caller has already
+// waited for the copies that matter, and lgkmcnt(0) retires this wave's LDS
+// reads, so a plain s_barrier suffices. The memory clobber keeps the compiler
+// from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int BN, int WAVES_M, int S, bool OUT16, bool DUMP>
+__global__ __launch_bounds__(128 * WAVES_M, 512 / (128 * WAVES_M)) void w8a8_dma_kernel(W8A8Args a) {
+    using C = DmaCfg<BN, WAVES_M>;
+    constexpr int BM = C::BM, BK = C::BK;
+    constexpr int WM = 128, WN = BN / 2;
+    constexpr int FM = WM / 32, FN = WN / 32;
+    static_assert(S >= 2 && S <= 3, "2 or 3 stages");
+    static_assert(S == 2 || WAVES_M == 2, "uneven copy counts per wave need S == 2 (vmcnt(0))");
+    __shared__ __attribute__((aligned(1024))) uint8_t st0[C::kStageBytes];
+    __shared__ __attribute__((aligned(1024))) uint8_t st1[C::kStageBytes];
+    __shared__ __attribute__((aligned(1024))) uint8_t st2[S > 2 ? C::kStageBytes : 1024];
+    __shared__ __attribute__((aligned(16))) float sRowScale[BM];
+    __shared__ __attribute__((aligned(16))) int sRowSum[BM];
+    __shared__ float sColScale[BN];
+    __shared__ int sColZero[BN];
+    __shared__ float sColBias[BN];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;  // 2 waves across the columns
+    const int tiles_m = (int)((a.rows + BM - 1) / BM);
+    const int tiles_n = (int)((a.columns + BN - 1) / BN);
+    const int K = (int)a.width;
+    const int ktiles = K / BK;
+    const bool has_bias = a.bias != nullptr;
+    const bool has_zero = a.w_zero != nullptr;
+    constexpr int kGroupM = 4;
+
+    const int l = xcd_remap(blockIdx.x, tiles_m * tiles_n);
+    const int group_size = kGroupM * tiles_n;
+    const int first_m = (l / group_size) * kGroupM;
+    const int gm = min(tiles_m - first_m, kGroupM);
+    const int64_t m0 = (int64_t)__builtin_amdgcn_readfirstlane(first_m + (l % group_size) % gm) * BM;
+    const int64_t n0 = (int64_t)__builtin_amdgcn_readfirstlane((l % group_size) / gm) * BN;
+
+    // Copy sources: wave w copies A rows [16*kACopies*w, ...) as kACopies
+    // blocks of 16 rows; waves 0..3 copy W rows [BN/4 * w, ...) as kBCopies
+    // blocks. Rows past the matrix are clamped (their accumulators are never
+    // stored).
+    const int cp_row = lane >> 2;
+    const int cp_chunk = (lane & 3) ^ ((lane >> 4) & 3);
+    const uint8_t* srcA[C::kACopies];
+    const uint8_t* srcB[C::kBCopies];
+#pragma unroll
+    for (int i = 0; i < C::kACopies; ++i) {
+        const int64_t r = min(m0 + (wave * C::kACopies + i) * 16 + cp_row, a.rows - 1);
+        srcA[i] = a.x + r * K + cp_chunk * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < C::kBCopies; ++i) {
+        const int64_t r = min(n0 + (wave & 3) * (BN / 4) + i * 16 + cp_row, a.columns - 1);
+        srcB[i] = a.w + r * K + cp_chunk * 16;
+    }
+    // Copy K tile kt (clamped to the last, so that every K tile issues the
+    // same number of copies) into stage buffer dst.
+    auto copy_tile = [&](int kt, uint8_t* dst) {
+        const int k0 = min(kt, ktiles - 1) * BK;
+#pragma unroll
+        for (int i = 0; i < C::kACopies; ++i)
+            lds_copy16(srcA[i] + k0, dst + ((wave * C::kACopies + i) * 16) * BK);
+        if (wave < 4) {
+#pragma unroll
+            for (int i = 0; i < C::kBCopies; ++i)
+                lds_copy16(srcB[i] + k0, dst + BM * BK + (wave * (BN / 4) + i * 16) * BK);
+        }
+    };
+
+    // Epilogue values, staged in LDS before the K loop (their loads are the
+    // first vector-memory operations, so the K loop's waits cover them).
+    {
+        const int64_t row = min(m0 + tid, (int64_t)a.rows - 1);
+        sRowScale[tid] = a.x_scale[row];
+        sRowSum[tid] = has_zero ? a.x_sum[row] : 0;
+        if (tid < BN) {
+            const int64_t col = min(n0 + tid, (int64_t)a.columns - 1);
+            sColScale[tid] = a.w_scale[col];
+            sColZero[tid] = has_zero ? a.w_zero[col] : 0;
+            sColBias[tid] = has_bias ? a.bias[col] : 0.0f;
+        }
+    }
+
+    __syncthreads();  // params visible to all waves (before any copy is in flight)
+    copy_tile(0, st0);
+    if constexpr (S > 2) copy_tile(1, st1);
+
+    // Fragment read bases (the same swizzled layout as the register-staged kernel).
+    const int fr = lane & 31, fh = lane >> 5, fq = (fr >> 2) & 3;
+    const int fragA0 = (wm * WM + fr) * BK + (((0 + fh) ^ fq) << 4);
+    const int fragA1 = (wm * WM + fr) * BK + (((2 + fh) ^ fq) << 4);
+    const int fragB0 = BM * BK + (wn * WN + fr) * BK + (((0 + fh) ^ fq) << 4);
+    const int fragB1 = BM * BK + (wn * WN + fr) * BK + (((2 + fh) ^ fq) << 4);
+
+    v16i acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
+
+    auto stage = [&](int b) -> uint8_t* { return b == 0 ? st0 : b == 1 ? st1 : st2; };
+    for (int t0 = 0; t0 < ktiles; t0 += S) {
+#pragma unroll
+        for (int u = 0; u < S; ++u) {
+            const int kt = t0 + u;
+            // K tiles kt .. kt+S-2 are in flight; wait for kt's copies and for
+            // this wave's reads of the previous stage, then for every wave.
+            s_waitcnt_vm<(S - 2) * (C::kACopies + C::kBCopies), true>();
+            lds_barrier();  // all copies of kt landed; stage (u - 1) % S is free
+            copy_tile(kt + S - 1, stage((u + S - 1) % S));
+            const uint8_t* tb = stage(u);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                v4i fa[FM], fb[FN];
+                const uint8_t* pa = tb + (ks ? fragA1 : fragA0);
+                const uint8_t* pb = tb + (ks ? fragB1 : fragB0);
+#pragma unroll
+                for (int i = 0; i < FM; ++i) fa[i] = *reinterpret_cast<const v4i*>(pa + i * 32 * BK);
+#pragma unroll
+                for (int j = 0; j < FN; ++j) fb[j] = *reinterpret_cast<const v4i*>(pb + j * 32 * BK);
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+            }
+        }
+    }
+
+    // 32x32 accumulator layout: lane holds column (lane & 31) and rows
+    // 8*(r/4) + 4*(lane/32) + (r%4) of each 32x32 block. Offsets are 32-bit,
+    // relative to the tile's first element (host: 256 * columns < 2^31).
+    const int N = (int)a.columns;
+    const int64_t tile_base = m0 * a.columns + n0;
+    const bool full = m0 + BM <= a.rows && n0 + BN <= a.columns;
+    const int rows_left = (int)min((int64_t)BM, a.rows - m0);
+    const int cols_left = (int)min((int64_t)BN, a.columns - n0);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int lr0 = wm * WM + i * 32 + 4 * fh;
+            const int lc = wn * WN + j * 32 + fr;
+            const float ws = sColScale[lc];
+            const int zero = sColZero[lc];
+            const float bias = sColBias[lc];
+            const int base = lr0 * N + lc;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 s4 = *reinterpret_cast<const float4*>(sRowScale + lr0 + 8 * q);
+                const int4 z4 = *reinterpret_cast<const int4*>(sRowSum + lr0 + 8 * q);
+                const float rs[4] = {s4.x, s4.y, s4.z, s4.w};
+                const int rsum[4] = {z4.x, z4.y, z4.z, z4.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int dr = 8 * q + e;
+                    const int off = base + dr * N;
+                    const int v = acc[i][j][4 * q + e];
+                    const float o = w8a8_epilogue(v, rsum[e], zero, rs[e], ws, bias, has_bias);
+                    if (full || (lr0 + dr < rows_left && lc < cols_left)) {
+                        if constexpr (DUMP) a.acc_dump[tile_base + off] = v;
+                        if constexpr (OUT16)
+                            static_cast<_Float16*>(a.out)[tile_base + off] = (_Float16)o;
+                        else
+                            static_cast<float*>(a.out)[tile_base + off] = o;
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // The clamped copies of the last K tiles may still be landing in LDS;
+    // drain them before the workgroup's LDS is released.
+    s_waitcnt_vm<0>();
+}
+
 // Compute units of the current device (cached per device).
 int num_cus() {
     static int cached[64] = {0};
@@ -398,13 +623,12 @@ int num_cus() {
     return cached[dev];
 }
 
-// OMNI_W8A8_TILE=<n> pins one tile configuration (tuning aid; 0 = heuristic).
+// OMNI_W8A8_TILE=<n> pins one tile configuration (tuning and test aid;
+// 0 or unset = the shape heuristic). Read on every launch so a process can
+// exercise each kernel variant in turn.
 int w8a8_tile_override() {
-    static const int value = [] {
-        const char* v = std::getenv("OMNI_W8A8_TILE");
-        return v ? std::atoi(v) : 0;
-    }();
-    return value;
+    const char* v = std::getenv("OMNI_W8A8_TILE");
+    return v ? std::atoi(v) : 0;
 }
 
 template <int BN, int PF, bool KTAIL, bool OUT16, bool DUMP>
@@ -425,6 +649,34 @@ hipError_t launch_cfg(const W8A8Args& a, hipStream_t stream) {
     const int64_t grid = tiles < num_cus() ? tiles : num_cus();
     hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(256), smem, stream, a);
     return hipGetLastError();
+}
+
+template <int BN, int WAVES_M, int S, bool OUT16, bool DUMP>
+hipError_t launch_dma_cfg(const W8A8Args& a, hipStream_t stream) {
+    constexpr int BM = 128 * WAVES_M;
+    const int64_t tiles = ((a.rows + BM - 1) / BM) * ((a.columns + BN - 1) / BN);
+    hipLaunchKernelGGL((w8a8_dma_kernel<BN, WAVES_M, S, OUT16, DUMP>), dim3((unsigned)tiles),
+                       dim3(128 * WAVES_M), 0, stream, a);
+    return hipGetLastError();
+}
+
+// The DMA kernel's K loop takes whole groups of S K tiles of 64 bytes.
+bool dma_fits(const W8A8Args& a, int S) {
+    return a.width % 64 == 0 && a.width >= 64 * S && (a.width / 64) % S == 0;
+}
+
+template <int BN, int PF>
+hipError_t launch_bn(const W8A8Args& a, hipStream_t stream);
+
+template <int BN, int S, int WAVES_M = 2>
+hipError_t launch_dma(const W8A8Args& a, hipStream_t stream) {
+    if (!dma_fits(a, S)) return launch_bn<BN == 128 ? 128 : 192, 2>(a, stream);
+    if (a.acc_dump) {
+        if (a.out_f16) return launch_dma_cfg<BN, WAVES_M, S, true, true>(a, stream);
+        return launch_dma_cfg<BN, WAVES_M, S, false, true>(a, stream);
+    }
+    if (a.out_f16) return launch_dma_cfg<BN, WAVES_M, S, true, false>(a, stream);
+    return launch_dma_cfg<BN, WAVES_M, S, false, false>(a, stream);
 }
 
 template <int BN, int PF, bool OUT16, bool DUMP>
@@ -462,20 +714,47 @@ hipError_t launch_w8a8_mfma(const W8A8Args& a, hipStream_t stream) {
         case 3: return launch_bn<192, 2>(a, stream);
         case 4: return launch_bn<128, 2>(a, stream);
         case 5: return launch_bn<192, 1>(a, stream);
+        case 6: return launch_dma<128, 3>(a, stream);
+        case 7: return launch_dma<192, 2>(a, stream);
+        case 8: return launch_dma<128, 2>(a, stream);
+        case 9: return launch_dma<192, 2, 4>(a, stream);
+        case 10: return launch_dma<128, 2, 4>(a, stream);
         default: break;
     }
-    // Column tile: the one whose tiles fill the CUs best (useful work over the
-    // work of the rounds of tiles launched), wider on ties. 256-wide tiles
-    // need every AGPR for accumulators and are kept for the override only.
+    // Candidates, in order of preference on equal CU fill (measured on
+    // MI355X: the LDS-DMA kernels move fewer L2 bytes per MFMA op):
+    //   DMA 512 x 192 (one 8-wave workgroup per CU), DMA 512 x 128,
+    //   DMA 256 x 192 (two workgroups per CU), register-staged 256 x 192 and
+    //   256 x 128 (one per CU). Fill = tiles / (rounds x concurrent slots).
     const int64_t cus = num_cus();
-    const int64_t tm = (a.rows + 255) / 256;
-    auto fill = [&](int64_t bn) {  // columns / (launched tile rounds x cus x bn) per tile row
-        const int64_t tn = (a.columns + bn - 1) / bn;
-        const int64_t rounds = (tm * tn + cus - 1) / cus;
-        return (double)a.columns * (double)tm / ((double)rounds * (double)cus * (double)bn);
+    auto fill = [&](int64_t bm, int64_t bn, int64_t per_cu) {
+        const int64_t tiles = ((a.rows + bm - 1) / bm) * ((a.columns + bn - 1) / bn);
+        const int64_t slots = cus * per_cu;
+        const int64_t rounds = (tiles + slots - 1) / slots;
+        // useful output area over the area the launched rounds could cover
+        return (double)(a.rows * a.columns) / ((double)rounds * (double)slots * (double)(bm * bn));
     };
-    if (fill(192) >= fill(128) * 0.97) return launch_bn<192, 2>(a, stream);
-    return launch_bn<128, 2>(a, stream);
+    // Each candidate's fill is weighted by its measured per-tile speed
+    // relative to the DMA 512 x 192 kernel (north_star shapes on MI355X).
+    struct Cand { double f; int id; };
+    Cand best{-1.0, 0};
+    auto consider = [&](double f, int id) {
+        if (f > best.f) best = Cand{f, id};
+    };
+    if (dma_fits(a, 2)) {
+        consider(1.00 * fill(512, 192, 1), 1);
+        consider(0.92 * fill(512, 128, 1), 2);
+        consider(0.95 * fill(256, 192, 2), 3);
+    }
+    consider(0.80 * fill(256, 192, 1), 4);
+    consider(0.75 * fill(256, 128, 1), 5);
+    switch (best.id) {
+        case 1: return launch_dma<192, 2, 4>(a, stream);
+        case 2: return launch_dma<128, 2, 4>(a, stream);
+        case 3: return launch_dma<192, 2>(a, stream);
+        case 4: return launch_bn<192, 2>(a, stream);
+        default: return launch_bn<128, 2>(a, stream);
+    }
 }
 
 }  // namespace omni

@@ -95,6 +95,25 @@ def test_quantize_rows_near_ties_at_random_scales(oracle):
     assert np.array_equal(host(total), ototal)
 
 
+@pytest.mark.parametrize("width", [256, 4096, 12288, 20000])
+def test_quantize_rows_nan_and_inf(oracle, width):
+    # Rust's f32::max skips NaN in the peak, and a NaN code converts to 0
+    # (int8_host.rs:3-10); an Inf peak makes every finite code 0.
+    rng = np.random.default_rng(width)
+    x = rng.standard_normal((6, width)).astype(np.float32)
+    x[0, 3] = np.nan
+    x[1, 5] = np.inf
+    x[2, 7] = -np.inf
+    x[3, :] = np.nan
+    x[4, 1] = np.nan
+    x[4, 2] = np.inf
+    codes, rs, total = oi.quantize_rows(dev(x))
+    ocodes, ors, ototal = oracle.quantize_rows(x)
+    assert np.array_equal(host(codes), ocodes)
+    assert np.array_equal(host(rs).view(np.uint32), ors.view(np.uint32))
+    assert np.array_equal(host(total), ototal)
+
+
 # -- the reference's own tests ------------------------------------------------------
 
 
@@ -184,6 +203,30 @@ def test_w8a8_extreme_codes_no_overflow(oracle):
     zero = np.zeros(40, np.int32)
     codes, rs, total, out, acc = run_gemm(x, w, scale, zero, lowering=oi.OMNI_LOWERING_MFMA)
     assert np.array_equal(acc, oracle.int8_acc(codes, w))
+
+
+# Every MFMA kernel variant (OMNI_W8A8_TILE; 0 = the shape heuristic) on
+# shapes with ragged M/N edges, K tails and multi-round tile grids.
+VARIANT_SHAPES = [(300, 1024, 700), (1000, 4096, 1500), (513, 4160, 389), (700, 3072, 650),
+                  (2048, 2048, 3072)]
+
+
+@pytest.mark.parametrize("tile", list(range(0, 11)))
+def test_w8a8_every_kernel_variant(oracle, tile, monkeypatch):
+    monkeypatch.setenv("OMNI_W8A8_TILE", str(tile))
+    for rows, width, columns in VARIANT_SHAPES:
+        rng = np.random.default_rng(tile * 100 + rows)
+        x = rng.standard_normal((rows, width)).astype(np.float16)
+        w = rng.integers(-128, 128, (columns, width), dtype=np.int8)
+        scale = rng.uniform(0.002, 0.02, columns).astype(np.float32)
+        zero = rng.integers(-3, 4, columns).astype(np.int32)
+        codes, rs, total = oi.quantize_rows(dev(x))
+        out, acc = oi.w8a8_gemm(codes, rs, total, dev(w), dev(scale), dev(zero), acc_dump=True,
+                                lowering=oi.OMNI_LOWERING_MFMA)
+        exact = codes.double() @ dev(w).double().T
+        assert torch.equal(acc.double(), exact), (tile, rows, width, columns)
+        ref = ((acc - total[:, None] * dev(zero)[None, :]).float() * rs[:, None]) * dev(scale)[None, :]
+        assert torch.equal(out.view(torch.int32), ref.view(torch.int32)), (tile, rows, width, columns)
 
 
 # -- BASELINE configs at full size ---------------------------------------------------
