@@ -126,7 +126,8 @@ int omni_try_int8_gemm(const void* x, int x_dtype, int64_t rows, int64_t width,
  *   out[m][n] = f16(scale[n] * sum_k x[m][k] * w[n][k] + bias[n])
  * x f16 [rows][width], w int8 [columns][width], scale f16 [columns],
  * bias f16 [columns] or NULL, out f16 [rows][columns]. width % 16 == 0.
- * rows <= 16 runs the HBM-bound GEMV; larger rows run the fp16-MFMA GEMM. */
+ * rows <= 4 with width <= 16384 runs the HBM-bound GEMV; other shapes run the
+ * fp16-MFMA GEMM. */
 int omni_w8a16_gemm(const uint16_t* x, const int8_t* w, const uint16_t* scale,
                     const uint16_t* bias, int64_t rows, int64_t columns, int64_t width,
                     uint16_t* out, void* stream);

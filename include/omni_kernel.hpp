@@ -95,7 +95,8 @@ namespace int8_matmul {
 // crates/omni-kernel/src/int8_matmul.rs:505-560. w_packed holds n * (k / 4)
 // little-endian int8 groups (int32 words); w_scale (f32) and w_zero (int32)
 // are per output row. Returns an f32 [rows, n] tensor allocated from
-// `alloc`, or std::nullopt when the shapes disagree (:517-521). x may be f32
+// `alloc`, or std::nullopt when the shapes disagree (:517-521) or the current
+// device is not gfx950. x may be f32
 // or f16 (f16 is exact in f32; the reference casts to f32 first, :525).
 inline std::optional<DeviceTensor> try_int8_gemm(const DeviceTensor& x, const DeviceTensor& w_packed,
                                                  const DeviceTensor& w_scale,
@@ -120,7 +121,9 @@ inline std::optional<DeviceTensor> try_int8_gemm(const DeviceTensor& x, const De
                                       w_zero.dim(0), static_cast<float*>(out.data), ws, ws_bytes,
                                       stream);
     alloc.release(ws, stream);
-    if (st == OMNI_NOT_HANDLED) {
+    // Shape disagreement, or a device this library does not serve: the
+    // reference's None (int8_matmul.rs:517-521, :494-503).
+    if (st == OMNI_NOT_HANDLED || st == OMNI_NO_DEVICE) {
         alloc.release(out.data, stream);
         return std::nullopt;
     }
