@@ -7,20 +7,24 @@
 // (the reference's output) or rounded once to f16.
 //
 // Two lowerings, as the reference has two (int8_dot and int8_dot_tile64):
-//  * w8a8_mfma_kernel — the int8 MFMA path. Both operands are K-contiguous
-//    ("NT"), which is the layout v_mfma_i32_32x32x32_i8 wants for A and B
-//    alike: each lane feeds 16 consecutive k bytes of one row of A and one
-//    row of W. K tiles are staged through LDS (double-buffered, one barrier
-//    per K tile) with an XOR swizzle of the 16-byte chunk index so both the
-//    row-wise global->LDS writes and the column-of-rows fragment reads are
-//    bank-conflict free. The epilogue runs on the accumulators in registers,
-//    so no int32 accumulator array ever reaches HBM (the reference's tile64
-//    lowering round-trips one, int8_matmul.rs:423-439).
+//  * the int8 MFMA path (v_mfma_i32_32x32x32_i8). Both operands are
+//    K-contiguous ("NT"), the layout the instruction wants for A and B alike:
+//    each lane feeds 16 consecutive k bytes of one row of X and one row of W.
+//    K tiles are staged through LDS with an XOR swizzle of the 16-byte chunk
+//    index so both the global->LDS writes and the fragment reads are
+//    bank-conflict free, and the epilogue runs on the accumulators in
+//    registers, so no int32 accumulator array ever reaches HBM (the
+//    reference's tile64 lowering round-trips one, int8_matmul.rs:423-439).
+//    Three kernels cover the shapes: w8a8_ring_kernel (persistent, 256 x BN
+//    tiles, a 3-4 stage LDS-DMA ring), w8a8_dma_kernel (512 x BN tiles, two
+//    waves per SIMD) and w8a8_mfma_kernel (register-staged copies; any
+//    K % 16 == 0). launch_w8a8_mfma picks one with a cost model.
 //  * w8a8_scalar_kernel — v_dot4_i32_i8 per thread, the analog of the
 //    reference's scalar int8_dot; it serves widths that are not a multiple of
 //    16 and the OMNI_INT8_FORCE_SCALAR override.
 #include <atomic>
 #include <cstdlib>
+#include <type_traits>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -384,9 +388,9 @@ __global__ __launch_bounds__(256, 1) void w8a8_mfma_kernel(W8A8Args a) {
     }
 }
 
-// LDS-DMA GEMM (K % 64 == 0): one 256 x BN output tile per workgroup, two
-// workgroups per CU so that one's epilogue and pipeline ramp overlap the
-// other's K loop. K tiles are copied global -> LDS by global_load_lds_dwordx4:
+// LDS-DMA GEMM (K % 64 == 0): one 128*WAVES_M x BN output tile per workgroup
+// of 2*WAVES_M waves (512 x BN with 8 waves, two per SIMD, is the one the
+// launcher uses: one wave's MFMAs cover the other's copies). K tiles are copied global -> LDS by global_load_lds_dwordx4:
 // no staging registers and no LDS write instructions. A wave's copy
 // instruction fills a contiguous 1 KiB block (16 tile rows of 64 bytes, lane
 // l at byte 16*l), so the bank swizzle is applied on the global side: lane l
@@ -609,6 +613,287 @@ __global__ __launch_bounds__(128 * WAVES_M, 512 / (128 * WAVES_M)) void w8a8_dma
     s_waitcnt_vm<0>();
 }
 
+// Persistent LDS-DMA ring GEMM (K % 64 == 0, S divides the K-tile count).
+// One workgroup of 4 waves per CU walks 256 x BN output tiles; each wave owns
+// a 128 x BN/2 block of 32x32 int32 accumulators (AGPRs). K tiles of 64 bytes
+// reach LDS through global_load_lds_dwordx4 into an S-stage ring (S-1 tiles
+// in flight, distinct LDS arrays so each copy and read names its stage
+// statically). Per K tile the schedule is
+//   MFMAs (tile kt, k step 0)    | fragment reads (tile kt, k step 1)
+//   wait for tile kt+1's copies, barrier
+//   MFMAs (tile kt, k step 1)    | copy tile kt+S-1 into the freed stage,
+//                                | fragment reads (tile kt+1, k step 0)
+// so every LDS read has a whole MFMA group to land and the only barrier sits
+// between two MFMA groups. The next output tile's first copies are issued
+// before this tile's epilogue, whose per-row and per-column values sit in a
+// parity-double-buffered LDS block. Epilogue stores of partial tiles are
+// unconditional too: rows and columns past the matrix were loaded clamped to
+// the last row and column, so their values equal the last row's (column's)
+// and are stored there, a duplicate write of the same value.
+template <int BN, int S, bool OUT16, bool DUMP>
+__global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
+    constexpr int BM = 256, BK = 64;
+    constexpr int WM = 128, WN = BN / 2;
+    constexpr int FM = WM / 32, FN = WN / 32;
+    constexpr int kRows = BM + BN;            // tile rows per stage (A then W)
+    constexpr int kStage = kRows * BK;
+    constexpr int kCpw = kRows / 16 / 4;      // 1 KiB copies per wave per K tile
+    static_assert(kRows % 64 == 0 && WN % 32 == 0, "tile shape");
+    static_assert(S >= 3 && S <= 5, "3 to 5 stages");
+    __shared__ __attribute__((aligned(1024))) uint8_t st0[kStage];
+    __shared__ __attribute__((aligned(1024))) uint8_t st1[kStage];
+    __shared__ __attribute__((aligned(1024))) uint8_t st2[kStage];
+    __shared__ __attribute__((aligned(1024))) uint8_t st3[S > 3 ? kStage : 1024];
+    __shared__ __attribute__((aligned(1024))) uint8_t st4[S > 4 ? kStage : 1024];
+    __shared__ __attribute__((aligned(16))) float sRowScale[2][BM];
+    __shared__ __attribute__((aligned(16))) int sRowSum[2][BM];
+    __shared__ float sColScale[2][BN];
+    __shared__ int sColZero[2][BN];
+    __shared__ float sColBias[2][BN];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: an SGPR
+    const int wm = wave >> 1, wn = wave & 1;
+    const int tiles_m = (int)((a.rows + BM - 1) / BM);
+    const int tiles_n = (int)((a.columns + BN - 1) / BN);
+    const int total = tiles_m * tiles_n;
+    const int K = (int)a.width;
+    const int ktiles = K / BK;
+    const bool has_bias = a.bias != nullptr;
+    const bool has_zero = a.w_zero != nullptr;
+    constexpr int kGroupM = 4;
+
+    auto stage = [&](int s) -> uint8_t* {
+        return s == 0 ? st0 : s == 1 ? st1 : s == 2 ? st2 : s == 3 ? st3 : st4;
+    };
+
+    // Copy c (0 .. kRows/16) fills stage rows 16c .. 16c+15; this wave owns
+    // copies wave*kCpw + j. Lane l reads logical chunk (l%4) ^ ((l/16)%4) of
+    // row l/4, landing at physical chunk l%4 (the fragment reads' swizzle).
+    const int cp_row = lane >> 2;
+    const int cp_chunk = (lane & 3) ^ ((lane >> 4) & 3);
+    const uint8_t* src[kCpw];
+    int64_t m0 = 0, n0 = 0;
+    float p_rs = 0.0f, p_cs = 0.0f, p_cb = 0.0f;
+    int p_rsum = 0, p_cz = 0;
+    auto tile_origin = [&](int l, int64_t& tm0, int64_t& tn0) {
+        const int group_size = kGroupM * tiles_n;
+        const int first_m = (l / group_size) * kGroupM;
+        const int gm = min(tiles_m - first_m, kGroupM);
+        tm0 = (int64_t)__builtin_amdgcn_readfirstlane(first_m + (l % group_size) % gm) * BM;
+        tn0 = (int64_t)__builtin_amdgcn_readfirstlane((l % group_size) / gm) * BN;
+    };
+    // Copy sources of the tile at (m0, n0). Which matrix a copy reads and its
+    // first row are wave-uniform (scalar selects, no branches).
+    auto setup_copies = [&]() {
+#pragma unroll
+        for (int j = 0; j < kCpw; ++j) {
+            const int c16 = (wave * kCpw + j) * 16;  // first stage row of copy j
+            const bool is_a = c16 < BM;
+            const uint8_t* base = is_a ? a.x : a.w;
+            const int64_t first = is_a ? m0 + c16 : n0 + (c16 - BM);
+            const int64_t last = is_a ? a.rows - 1 : a.columns - 1;
+            const int64_t row = min(first + cp_row, last);
+            src[j] = base + row * K + cp_chunk * 16;
+        }
+    };
+    // Epilogue values of the tile at (pm0, pn0) into registers: thread tid
+    // holds row tid's and column tid's.
+    auto load_params = [&](int64_t pm0, int64_t pn0) {
+        const int64_t row = min(pm0 + tid, a.rows - 1);
+        p_rs = a.x_scale[row];
+        p_rsum = has_zero ? a.x_sum[row] : 0;
+        if (tid < BN) {
+            const int64_t col = min(pn0 + tid, a.columns - 1);
+            p_cs = a.w_scale[col];
+            p_cz = has_zero ? a.w_zero[col] : 0;
+            p_cb = has_bias ? a.bias[col] : 0.0f;
+        }
+    };
+    auto store_params = [&](int p) {
+        sRowScale[p][tid] = p_rs;
+        sRowSum[p][tid] = p_rsum;
+        if (tid < BN) {
+            sColScale[p][tid] = p_cs;
+            sColZero[p][tid] = p_cz;
+            sColBias[p][tid] = p_cb;
+        }
+    };
+    auto copy_tile = [&](int kt, int s) {
+        const int k0 = min(kt, ktiles - 1) * BK;
+        uint8_t* dst = stage(s) + wave * kCpw * 1024;
+#pragma unroll
+        for (int j = 0; j < kCpw; ++j) lds_copy16(src[j] + k0, dst + j * 1024);
+    };
+
+    // Fragment read offsets within a stage, k steps 0 and 1.
+    const int fr = lane & 31, fh = lane >> 5, fq = (fr >> 2) & 3;
+    const int fragA0 = (wm * WM + fr) * BK + (((0 + fh) ^ fq) << 4);
+    const int fragA1 = (wm * WM + fr) * BK + (((2 + fh) ^ fq) << 4);
+    const int fragB0 = BM * BK + (wn * WN + fr) * BK + (((0 + fh) ^ fq) << 4);
+    const int fragB1 = BM * BK + (wn * WN + fr) * BK + (((2 + fh) ^ fq) << 4);
+    v4i fa0[FM], fb0[FN], fa1[FM], fb1[FN];
+    auto read_frags = [&](int s, int ks, v4i (&fa)[FM], v4i (&fb)[FN]) {
+        const uint8_t* pa = stage(s) + (ks ? fragA1 : fragA0);
+        const uint8_t* pb = stage(s) + (ks ? fragB1 : fragB0);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) fa[i] = *reinterpret_cast<const v4i*>(pa + i * 32 * BK);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) fb[j] = *reinterpret_cast<const v4i*>(pb + j * 32 * BK);
+    };
+
+    int L = xcd_remap(blockIdx.x, gridDim.x);
+    if (L >= total) return;
+    tile_origin(L, m0, n0);
+    setup_copies();
+    load_params(m0, n0);
+    store_params(0);
+#pragma unroll
+    for (int u = 0; u < S - 1; ++u) copy_tile(u, u);
+    int parity = 0;
+
+    while (true) {
+        const int Ln = L + gridDim.x;
+        const bool more = Ln < total;
+        int64_t nm0 = 0, nn0 = 0;
+        if (more) {
+            // The next tile's epilogue values, loaded a whole tile early.
+            tile_origin(Ln, nm0, nn0);
+            load_params(nm0, nn0);
+        }
+        v16i acc[FM][FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
+
+        // Tile 0's copies (and the parameter stores) visible to every wave.
+        s_waitcnt_vm<(S - 2) * kCpw, true>();
+        lds_barrier();
+        read_frags(0, 0, fa0, fb0);
+
+        for (int t0 = 0; t0 < ktiles; t0 += S) {
+#pragma unroll
+            for (int u = 0; u < S; ++u) {
+                const int kt = t0 + u;
+                // Each MFMA group starts with one MFMA on fragments that
+                // landed a group earlier, then issues the next group's reads,
+                // then the rest: the reads overlap the MFMAs and the wait for
+                // them falls at the next group's start. The scheduling
+                // barriers keep the compiler from sinking the reads to their
+                // first use.
+                acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0[0], fb0[0], acc[0][0], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                read_frags(u, 1, fa1, fb1);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        if (i | j)
+                            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0[i], fb0[j], acc[i][j], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                s_waitcnt_vm<(S - 3) * kCpw, true>();
+                lds_barrier();  // tile kt+1 landed everywhere; stage (u+S-1)%S is free
+                acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1[0], fb1[0], acc[0][0], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                copy_tile(kt + S - 1, (u + S - 1) % S);
+                read_frags((u + 1) % S, 0, fa0, fb0);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        if (i | j)
+                            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1[i], fb1[j], acc[i][j], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+
+        const int64_t em0 = m0, en0 = n0;
+        // Every wave is done reading the ring before the next tile's copies.
+        s_waitcnt_vm<(S - 2) * kCpw, true>();
+        lds_barrier();
+        if (more) {
+            m0 = nm0;
+            n0 = nn0;
+            setup_copies();
+            store_params(parity ^ 1);
+#pragma unroll
+            for (int u = 0; u < S - 1; ++u) copy_tile(u, u);
+        }
+
+        // Epilogue. 32x32 accumulator layout: lane holds column (lane & 31)
+        // and rows 8*(r/4) + 4*(lane/32) + (r%4) of each 32x32 block.
+        // Offsets are 32-bit, relative to the tile's first element (the host
+        // guarantees 256 * columns < 2^31).
+        const int N = (int)a.columns;
+        const int64_t tile_base = em0 * a.columns + en0;
+        int efr = fr, efh = fh;
+        asm volatile("" : "+v"(efr), "+v"(efh));
+        const bool full = em0 + BM <= a.rows && en0 + BN <= a.columns;
+        const int rows_last = (int)min((int64_t)BM, a.rows - em0) - 1;
+        const int cols_last = (int)min((int64_t)BN, a.columns - en0) - 1;
+        const float* pRowScale = sRowScale[parity];
+        const int* pRowSum = sRowSum[parity];
+        const float* pColScale = sColScale[parity];
+        const int* pColZero = sColZero[parity];
+        const float* pColBias = sColBias[parity];
+        float* out32 = static_cast<float*>(a.out) + tile_base;
+        _Float16* out16 = static_cast<_Float16*>(a.out) + tile_base;
+        int32_t* dump = DUMP ? a.acc_dump + tile_base : nullptr;
+        auto epilogue = [&](auto clamp_tag) {
+            constexpr bool CLAMP = decltype(clamp_tag)::value;
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    const int lr0 = wm * WM + i * 32 + 4 * efh;
+                    int lc = wn * WN + j * 32 + efr;
+                    if constexpr (CLAMP) lc = min(lc, cols_last);
+                    const float ws = pColScale[lc];
+                    const int zero = pColZero[lc];
+                    const float bias = pColBias[lc];
+                    const unsigned base = (unsigned)(lr0 * N + lc);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float4 s4 = *reinterpret_cast<const float4*>(pRowScale + lr0 + 8 * q);
+                        const int4 z4 = *reinterpret_cast<const int4*>(pRowSum + lr0 + 8 * q);
+                        const float rs[4] = {s4.x, s4.y, s4.z, s4.w};
+                        const int rsum[4] = {z4.x, z4.y, z4.z, z4.w};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            unsigned off;
+                            if constexpr (CLAMP)
+                                off = (unsigned)(min(lr0 + 8 * q + e, rows_last) * N + lc);
+                            else
+                                off = base + (unsigned)((8 * q + e) * N);
+                            const int v = acc[i][j][4 * q + e];
+                            const float o = w8a8_epilogue(v, rsum[e], zero, rs[e], ws, bias, has_bias);
+                            if constexpr (DUMP) dump[off] = v;
+                            if constexpr (OUT16)
+                                out16[off] = (_Float16)o;
+                            else
+                                out32[off] = o;
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        };
+        if (full)
+            epilogue(std::false_type{});
+        else
+            epilogue(std::true_type{});
+        if (!more) break;
+        L = Ln;
+        parity ^= 1;
+    }
+    // Copies of clamped K tiles may still be landing; drain before exit.
+    s_waitcnt_vm<0>();
+}
+
 // Compute units of the current device (cached per device).
 int num_cus() {
     static int cached[64] = {0};
@@ -668,6 +953,32 @@ bool dma_fits(const W8A8Args& a, int S) {
 template <int BN, int PF>
 hipError_t launch_bn(const W8A8Args& a, hipStream_t stream);
 
+template <int BN, int S, bool OUT16, bool DUMP>
+hipError_t launch_ring_cfg(const W8A8Args& a, hipStream_t stream) {
+    const int64_t tiles = ((a.rows + 255) / 256) * ((a.columns + BN - 1) / BN);
+    // Persistent: one workgroup per CU (the kernel's occupancy is one).
+    const int64_t grid = tiles < num_cus() ? tiles : num_cus();
+    hipLaunchKernelGGL((w8a8_ring_kernel<BN, S, OUT16, DUMP>), dim3((unsigned)grid), dim3(256), 0,
+                       stream, a);
+    return hipGetLastError();
+}
+
+// The ring kernel's K loop takes whole groups of S K tiles of 64 bytes.
+bool ring_fits(const W8A8Args& a, int S) {
+    return a.width % 64 == 0 && a.width >= 64 * S && (a.width / 64) % S == 0;
+}
+
+template <int BN, int S>
+hipError_t launch_ring(const W8A8Args& a, hipStream_t stream) {
+    if (!ring_fits(a, S)) return launch_bn<BN == 128 ? 128 : 192, 2>(a, stream);
+    if (a.acc_dump) {
+        if (a.out_f16) return launch_ring_cfg<BN, S, true, true>(a, stream);
+        return launch_ring_cfg<BN, S, false, true>(a, stream);
+    }
+    if (a.out_f16) return launch_ring_cfg<BN, S, true, false>(a, stream);
+    return launch_ring_cfg<BN, S, false, false>(a, stream);
+}
+
 template <int BN, int S, int WAVES_M = 2>
 hipError_t launch_dma(const W8A8Args& a, hipStream_t stream) {
     if (!dma_fits(a, S)) return launch_bn<BN == 128 ? 128 : 192, 2>(a, stream);
@@ -709,51 +1020,55 @@ hipError_t launch_w8a8_scalar(const W8A8Args& a, hipStream_t stream) {
 hipError_t launch_w8a8_mfma(const W8A8Args& a, hipStream_t stream) {
     if (a.rows == 0 || a.columns == 0) return hipSuccess;
     switch (w8a8_tile_override()) {
-        case 1: return launch_bn<256, 1>(a, stream);
-        case 2: return launch_bn<256, 2>(a, stream);
         case 3: return launch_bn<192, 2>(a, stream);
         case 4: return launch_bn<128, 2>(a, stream);
-        case 5: return launch_bn<192, 1>(a, stream);
-        case 6: return launch_dma<128, 3>(a, stream);
-        case 7: return launch_dma<192, 2>(a, stream);
-        case 8: return launch_dma<128, 2>(a, stream);
         case 9: return launch_dma<192, 2, 4>(a, stream);
         case 10: return launch_dma<128, 2, 4>(a, stream);
+        case 11: return launch_ring<256, 4>(a, stream);
+        case 12: return launch_ring<192, 4>(a, stream);
+        case 13: return launch_ring<128, 4>(a, stream);
+        case 14: return launch_ring<256, 3>(a, stream);
+        case 15: return launch_ring<192, 3>(a, stream);
         default: break;
     }
-    // Candidates, in order of preference on equal CU fill (measured on
-    // MI355X: the LDS-DMA kernels move fewer L2 bytes per MFMA op):
-    //   DMA 512 x 192 (one 8-wave workgroup per CU), DMA 512 x 128,
-    //   DMA 256 x 192 (two workgroups per CU), register-staged 256 x 192 and
-    //   256 x 128 (one per CU). Fill = tiles / (rounds x concurrent slots).
+    // Cost model, fitted to MI355X timings of every candidate on the BASELINE
+    // shapes: a kernel runs its tiles in rounds of one tile per CU; a round
+    // costs c * BM * BN (times K, common to all candidates), and a partial
+    // last round with fill f costs (0.5 + 0.5 f) of a full one (the chip is
+    // power-limited on this path, so a partly idle round runs at a higher
+    // clock). c is the measured cost per output element and K byte.
     const int64_t cus = num_cus();
-    auto fill = [&](int64_t bm, int64_t bn, int64_t per_cu) {
+    const int64_t kt = a.width % 64 == 0 ? a.width / 64 : 0;
+    auto cost = [&](double c, int64_t bm, int64_t bn) {
         const int64_t tiles = ((a.rows + bm - 1) / bm) * ((a.columns + bn - 1) / bn);
-        const int64_t slots = cus * per_cu;
-        const int64_t rounds = (tiles + slots - 1) / slots;
-        // useful output area over the area the launched rounds could cover
-        return (double)(a.rows * a.columns) / ((double)rounds * (double)slots * (double)(bm * bn));
+        const int64_t full = tiles / cus, rem = tiles % cus;
+        const double rounds = (double)full + (rem ? 0.5 + 0.5 * (double)rem / (double)cus : 0.0);
+        return c * (double)(bm * bn) * rounds;
     };
-    // Each candidate's fill is weighted by its measured per-tile speed
-    // relative to the DMA 512 x 192 kernel (north_star shapes on MI355X).
-    struct Cand { double f; int id; };
-    Cand best{-1.0, 0};
-    auto consider = [&](double f, int id) {
-        if (f > best.f) best = Cand{f, id};
+    struct Cand { double t; int id; };
+    Cand best{cost(364.0, 256, 192), 3};  // register-staged 256 x 192 takes any K % 16 == 0
+    auto consider = [&](bool ok, double t, int id) {
+        if (ok && t < best.t) best = Cand{t, id};
     };
-    if (dma_fits(a, 2)) {
-        consider(1.00 * fill(512, 192, 1), 1);
-        consider(0.92 * fill(512, 128, 1), 2);
-        consider(0.95 * fill(256, 192, 2), 3);
-    }
-    consider(0.80 * fill(256, 192, 1), 4);
-    consider(0.75 * fill(256, 128, 1), 5);
+    consider(true, cost(400.0, 256, 128), 4);
+    consider(dma_fits(a, 2), cost(266.0, 512, 192), 9);
+    consider(dma_fits(a, 2), cost(297.0, 512, 128), 10);
+    const bool s4 = kt >= 4 && kt % 4 == 0, s3 = kt >= 3 && kt % 3 == 0;
+    consider(s4, cost(289.0, 256, 256), 11);
+    consider(s4, cost(288.0, 256, 192), 12);
+    consider(s4, cost(323.0, 256, 128), 13);
+    consider(!s4 && s3, cost(298.0, 256, 256), 14);
+    consider(!s4 && s3, cost(297.0, 256, 192), 15);
     switch (best.id) {
-        case 1: return launch_dma<192, 2, 4>(a, stream);
-        case 2: return launch_dma<128, 2, 4>(a, stream);
-        case 3: return launch_dma<192, 2>(a, stream);
-        case 4: return launch_bn<192, 2>(a, stream);
-        default: return launch_bn<128, 2>(a, stream);
+        case 4: return launch_bn<128, 2>(a, stream);
+        case 9: return launch_dma<192, 2, 4>(a, stream);
+        case 10: return launch_dma<128, 2, 4>(a, stream);
+        case 11: return launch_ring<256, 4>(a, stream);
+        case 12: return launch_ring<192, 4>(a, stream);
+        case 13: return launch_ring<128, 4>(a, stream);
+        case 14: return launch_ring<256, 3>(a, stream);
+        case 15: return launch_ring<192, 3>(a, stream);
+        default: return launch_bn<192, 2>(a, stream);
     }
 }
 

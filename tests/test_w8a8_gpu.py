@@ -208,10 +208,11 @@ def test_w8a8_extreme_codes_no_overflow(oracle):
 # Every MFMA kernel variant (OMNI_W8A8_TILE; 0 = the shape heuristic) on
 # shapes with ragged M/N edges, K tails and multi-round tile grids.
 VARIANT_SHAPES = [(300, 1024, 700), (1000, 4096, 1500), (513, 4160, 389), (700, 3072, 650),
-                  (2048, 2048, 3072)]
+                  (2048, 2048, 3072), (4400, 512, 4100)]
+TILE_VARIANTS = [3, 4, 9, 10, 11, 12, 13, 14, 15]  # OMNI_W8A8_TILE values
 
 
-@pytest.mark.parametrize("tile", list(range(0, 11)))
+@pytest.mark.parametrize("tile", [0] + TILE_VARIANTS)
 def test_w8a8_every_kernel_variant(oracle, tile, monkeypatch):
     monkeypatch.setenv("OMNI_W8A8_TILE", str(tile))
     for rows, width, columns in VARIANT_SHAPES:
@@ -227,6 +228,25 @@ def test_w8a8_every_kernel_variant(oracle, tile, monkeypatch):
         assert torch.equal(acc.double(), exact), (tile, rows, width, columns)
         ref = ((acc - total[:, None] * dev(zero)[None, :]).float() * rs[:, None]) * dev(scale)[None, :]
         assert torch.equal(out.view(torch.int32), ref.view(torch.int32)), (tile, rows, width, columns)
+
+
+@pytest.mark.parametrize("tile", TILE_VARIANTS)
+def test_w8a8_every_kernel_variant_f16_bias(oracle, tile, monkeypatch):
+    # The f16-output and bias epilogue of each variant, on a ragged shape.
+    monkeypatch.setenv("OMNI_W8A8_TILE", str(tile))
+    rows, width, columns = 700, 3072, 650
+    rng = np.random.default_rng(tile)
+    x = rng.standard_normal((rows, width)).astype(np.float16)
+    w = rng.integers(-128, 128, (columns, width), dtype=np.int8)
+    scale = rng.uniform(0.002, 0.02, columns).astype(np.float32)
+    zero = rng.integers(-3, 4, columns).astype(np.int32)
+    bias = rng.standard_normal(columns).astype(np.float32)
+    codes, rs, total = oi.quantize_rows(dev(x))
+    out = oi.w8a8_gemm(codes, rs, total, dev(w), dev(scale), dev(zero), bias=dev(bias),
+                       out_dtype=torch.float16, lowering=oi.OMNI_LOWERING_MFMA)
+    _, o16 = oracle.w8a8_finish(oracle.int8_acc(host(codes), w), host(total), host(rs), scale, zero,
+                                bias)
+    assert np.array_equal(host(out).view(np.uint16), o16), tile
 
 
 # -- BASELINE configs at full size ---------------------------------------------------
