@@ -42,7 +42,21 @@ def parse():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="bounded CPU-baseline sample length")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only run a 256 MiB device copy (three times): the known-size kernel "
+                        "that scales rocprofv3's FETCH_SIZE / WRITE_SIZE readings")
     return p.parse_args()
+
+
+def copy_calibration():
+    import torch
+    x = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": x.numel(), "copies": 3}))
 
 
 def graph_of(fn, iters):
@@ -130,6 +144,9 @@ def cpu_gemv_baseline(oracle, np, seconds):
 
 def main():
     args = parse()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(the path shards by output columns across GPUs, see DESIGN.md)", file=sys.stderr)
