@@ -45,7 +45,47 @@ def parse():
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a 256 MiB device copy (three times): the known-size kernel "
                         "that scales rocprofv3's FETCH_SIZE / WRITE_SIZE readings")
+    p.add_argument("--gemm-data-sweep", action="store_true",
+                   help="only time the W8A8 GEMM of both north_star shapes on random and on "
+                        "constant operands (same kernels, same work): the card's power-managed "
+                        "clock follows operand bit toggling")
     return p.parse_args()
+
+
+def gemm_data_sweep(steps):
+    """The GEMM alone (quantised codes resident) on random codes and weights,
+    then on all-ones codes and weights, then random again; one JSON line."""
+    import torch
+    import omni_int8 as oi
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    stream = torch.cuda.current_stream(dev)
+    res = []
+    for M, K, N in GEMM_SHAPES:
+        rs = torch.rand(M, generator=gen, device=dev) * 0.01 + 0.001
+        total = torch.zeros(M, dtype=torch.int32, device=dev)
+        scale = torch.rand(N, generator=gen, device=dev) * 0.018 + 0.002
+        zero = torch.zeros(N, dtype=torch.int32, device=dev)
+        for kind in ("random", "ones", "random"):
+            if kind == "random":
+                codes = torch.randint(-127, 128, (M, K), generator=gen, device=dev, dtype=torch.int8)
+                w = torch.randint(-127, 128, (N, K), generator=gen, device=dev, dtype=torch.int8)
+            else:
+                codes = torch.ones((M, K), device=dev, dtype=torch.int8)
+                w = torch.ones((N, K), device=dev, dtype=torch.int8)
+
+            def one():
+                oi.w8a8_gemm(codes, rs, total, w, scale, zero)
+
+            for _ in range(10):
+                one()
+            g = graph_of(one, steps)
+            t = timed_graph(g, stream) / steps
+            del g
+            res.append({"M": M, "K": K, "N": N, "operands": kind, "gemm_us": round(t * 1e6, 2),
+                        "gemm_tops": round(2.0 * M * N * K / t / 1e12, 1)})
+    print(json.dumps({"gemm_data_sweep": res}))
 
 
 def copy_calibration():
@@ -146,6 +186,9 @@ def main():
     args = parse()
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.gemm_data_sweep:
+        gemm_data_sweep(args.steps)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
