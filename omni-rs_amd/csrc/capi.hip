@@ -229,8 +229,8 @@ int omni_w8a16_gemm(const uint16_t* x, const int8_t* w, const uint16_t* scale,
     a.columns = columns;
     a.width = width;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    // The GEMV keeps its slice of x in registers: 4 chunks of 16 per lane
-    // cover width <= 16384.
+    // The GEMV spreads a row over one workgroup of at most 1024 lanes, one
+    // 16-element chunk per lane: width <= 16384.
     if (rows <= 4 && width <= 16384)
         return hip_status(omni::launch_w8a16_gemv(a, s), "w8a16 gemv launch");
     return hip_status(omni::launch_w8a16_mfma(a, s), "w8a16 mfma launch");

@@ -88,27 +88,35 @@ __device__ __forceinline__ int fold_index(int lane) {
     return idx;
 }
 
-// MR activation rows (1, 2 or 4; unused rows are zero), CPL 16-element k
-// chunks per lane (the workgroup's 256 lanes own chunks tid + 256*j), R weight
-// rows per group. Weights of the next group are loaded while the current
-// group is reduced (PIPE).
-template <int MR, int CPL, int R, bool PIPE>
-__global__ __launch_bounds__(256) void w8a16_gemv_kernel(W8A16Args a) {
+// MR activation rows (1, 2 or 4; unused rows are zero). A workgroup of T
+// lanes (T = blockDim.x, a multiple of 64, at most 1024) owns R consecutive
+// weight rows; lane t owns the 16-element k chunks t + T*j, j < CPL, so one
+// row of W is T*CPL*16 bytes wide at most. Every weight load of the
+// workgroup is issued before any arithmetic (after x's chunks, which hit in
+// L2), as nontemporal loads (the weights are read once; keeping them out of
+// the caches keeps x and the scales there), so the whole workgroup's share
+// of W is in flight at once. One workgroup per row group, many of them
+// resident per CU, keeps the HBM queues full: measured on MI355X this
+// streams within a few percent of a bare read kernel of the same size, and
+// a 525 MB weight (a 128256 x 4096 vocabulary head) at 7.2 TB/s.
+template <int MR, int CPL, int R>
+__global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
     constexpr int V = R * MR;
     static_assert((V & (V - 1)) == 0 && V <= 64, "power-of-two partial count");
-    __shared__ float s_part[4][V];
+    __shared__ float s_part[16][V];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    const int T = blockDim.x;
     const int64_t K = a.width;
     const int64_t chunks = K / 16;
-    const int64_t groups = (a.columns + R - 1) / R;
+    const int64_t n0 = (int64_t)blockIdx.x * R;
 
-    // Resident x: for each owned chunk j and row m, 16 halves as 8 f16 pairs.
+    // x chunks: 16 halves of each owned chunk and row as 8 f16 pairs.
     v2h xr[CPL][MR][8];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        const int64_t c = tid + 256 * j;
+        const int64_t c = tid + (int64_t)T * j;
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
             if (c < chunks && m < a.rows) {
@@ -125,122 +133,103 @@ __global__ __launch_bounds__(256) void w8a16_gemv_kernel(W8A16Args a) {
         }
     }
 
-    auto load = [&](uint4 (&wv)[R][CPL], int64_t g) {
+    // Then every weight load. Rows past the matrix and chunks past K are
+    // clamped, not predicated (a predicated load lets the compiler pull its
+    // consumers next to it); clamped chunks meet zero activations.
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    v4u wv[R][CPL];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int64_t n0 = g * R + r;
-            const int64_t n = n0 < a.columns ? n0 : a.columns - 1;
-            const int8_t* wrow = a.w + n * K;
+    for (int r = 0; r < R; ++r) {
+        const int64_t n = n0 + r < a.columns ? n0 + r : a.columns - 1;
+        const int8_t* wrow = a.w + n * K;
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) {
-                // Clamped, not predicated: a predicated load lets the compiler
-                // pull its consumers next to it, which waits for it at once.
-                // Chunks past K meet zero activations, so their value is moot.
-                const int64_t c = tid + 256 * j < chunks ? tid + 256 * j : chunks - 1;
-                wv[r][j] = *reinterpret_cast<const uint4*>(wrow + c * 16);
-            }
+        for (int j = 0; j < CPL; ++j) {
+            const int64_t c = tid + (int64_t)T * j < chunks ? tid + (int64_t)T * j : chunks - 1;
+            wv[r][j] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wrow + c * 16));
         }
-    };
+    }
+    // This thread's epilogue row (tid / MR) % R: scale and bias.
+    const int64_t n_ep = min(n0 + (tid / MR) % R, a.columns - 1);
+    const _Float16 sc_h = a.scale[n_ep];
+    const _Float16 bi_h = (a.bias ? a.bias : a.scale)[n_ep];  // unconditional load
 
-    // Row groups blockIdx.x, blockIdx.x + gridDim.x, ... (measured faster on
-    // MI355X than giving each workgroup a contiguous range).
-    const int64_t g_begin = blockIdx.x, g_end = groups, g_step = gridDim.x;
-    // One row group: wait for its weights (cur), issue the next group's
-    // (nxt, unconditional: the last group re-reads itself from L2, so every
-    // path issues the same loads and the wait for cur leaves nxt in flight),
-    // then dot, reduce and store. The loop below alternates two register sets.
-    auto group = [&](uint4 (&cur)[R][CPL], uint4 (&nxt)[R][CPL], int64_t g) {
-        // This group's scale and bias, loaded by every thread (row tid % R)
-        // ahead of the next group's weights.
-        const int64_t n_ep = min(g * R + (tid / MR) % R, a.columns - 1);
-        const _Float16 sc_h = a.scale[n_ep];
-        const _Float16 bi_h = (a.bias ? a.bias : a.scale)[n_ep];  // unconditional load
-        if constexpr (PIPE) load(nxt, g + g_step < g_end ? g + g_step : g);
-        float part[V];
+    float part[V];
 #pragma unroll
-        for (int i = 0; i < V; ++i) part[i] = 0.0f;
+    for (int i = 0; i < V; ++i) part[i] = 0.0f;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
+    for (int r = 0; r < R; ++r) {
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) {
-                const u32 words[4] = {cur[r][j].x, cur[r][j].y, cur[r][j].z, cur[r][j].w};
+        for (int j = 0; j < CPL; ++j) {
+            const u32 words[4] = {wv[r][j].x, wv[r][j].y, wv[r][j].z, wv[r][j].w};
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    v2h w01, w23;
-                    i8x4_to_f16x4(words[q], w01, w23);
+            for (int q = 0; q < 4; ++q) {
+                v2h w01, w23;
+                i8x4_to_f16x4(words[q], w01, w23);
 #pragma unroll
-                    for (int m = 0; m < MR; ++m) {
-                        float& p = part[r * MR + m];
-                        p = __builtin_amdgcn_fdot2(w01, xr[j][m][2 * q], p, false);
-                        p = __builtin_amdgcn_fdot2(w23, xr[j][m][2 * q + 1], p, false);
-                    }
+                for (int m = 0; m < MR; ++m) {
+                    float& p = part[r * MR + m];
+                    p = __builtin_amdgcn_fdot2(w01, xr[j][m][2 * q], p, false);
+                    p = __builtin_amdgcn_fdot2(w23, xr[j][m][2 * q + 1], p, false);
                 }
             }
         }
-        Fold<V, 32>::run(part, lane);
-        if ((lane & (64 / V - 1)) == 0) s_part[wave][fold_index<V>(lane)] = part[0];
-        __syncthreads();
-        if (tid < V) {
-            const int r = tid / MR, m = tid % MR;
-            const int64_t n = g * R + r;
-            if (n < a.columns && m < a.rows) {
-                const float acc = s_part[0][tid] + s_part[1][tid] + s_part[2][tid] + s_part[3][tid];
-                const float bi = a.bias ? (float)bi_h : 0.0f;
-                a.out[(int64_t)m * a.columns + n] = (_Float16)(acc * (float)sc_h + bi);
-            }
-        }
-        __syncthreads();
-        if constexpr (!PIPE) {
-            if (g + g_step < g_end) load(cur, g + g_step);
-        }
-    };
-
-    uint4 wa[R][CPL], wb[R][CPL];
-    load(wa, g_begin);
-    for (int64_t g = g_begin; g < g_end; g += 2 * g_step) {
-        if constexpr (PIPE) {
-            group(wa, wb, g);
-            if (g + g_step < g_end) group(wb, wa, g + g_step);
-        } else {
-            group(wa, wa, g);
-            if (g + g_step < g_end) group(wa, wa, g + g_step);
+    }
+    Fold<V, 32>::run(part, lane);
+    if ((lane & (64 / V - 1)) == 0) s_part[wave][fold_index<V>(lane)] = part[0];
+    __syncthreads();
+    if (tid < V) {
+        const int r = tid / MR, m = tid % MR;
+        const int64_t n = n0 + r;
+        if (n < a.columns && m < a.rows) {
+            float acc = 0.0f;
+            for (int w = 0; w < T / 64; ++w) acc += s_part[w][tid];
+            const float bi = a.bias ? (float)bi_h : 0.0f;
+            a.out[(int64_t)m * a.columns + n] = (_Float16)(acc * (float)sc_h + bi);
         }
     }
 }
 
-// OMNI_W8A16_GRID=<n> pins the GEMV grid size (tuning aid; 0 = heuristic).
-int gemv_grid_override() {
-    static const int value = [] {
-        const char* v = std::getenv("OMNI_W8A16_GRID");
-        return v ? std::atoi(v) : 0;
-    }();
-    return value;
+// OMNI_W8A16_GEMV=<cpl><r> (e.g. 14 = one chunk per lane, four rows per
+// workgroup) pins the GEMV configuration (tuning aid; unset = heuristic).
+// Read on every launch so one process can time each configuration.
+int gemv_cfg_override() {
+    const char* v = std::getenv("OMNI_W8A16_GEMV");
+    return v ? std::atoi(v) : 0;
 }
 
-template <int MR, int CPL, int R, bool PIPE>
+template <int MR, int CPL, int R>
 hipError_t launch_gemv_cfg(const W8A16Args& a, hipStream_t stream) {
-    const int64_t groups = (a.columns + R - 1) / R;
-    // Up to 1024 workgroups (4 per CU), but at least two row groups per
-    // workgroup where there are enough, so that the next group's weights
-    // stream in while the current one is reduced (256-1024, measured).
-    int64_t grid = (groups + 1) / 2;
-    grid = grid < 256 ? 256 : (grid > 1024 ? 1024 : grid);
-    if (gemv_grid_override() > 0) grid = gemv_grid_override();
-    if (grid > groups) grid = groups;
-    hipLaunchKernelGGL((w8a16_gemv_kernel<MR, CPL, R, PIPE>), dim3((unsigned)grid), dim3(256), 0,
+    const int64_t chunks = a.width / 16;
+    const int64_t lanes = (chunks + CPL - 1) / CPL;
+    const int64_t T = ((lanes + 63) / 64) * 64;
+    if (T > 1024) return hipErrorInvalidValue;  // the caller keeps width <= 16384
+    const int64_t grid = (a.columns + R - 1) / R;
+    hipLaunchKernelGGL((w8a16_gemv_kernel<MR, CPL, R>), dim3((unsigned)grid), dim3((unsigned)T), 0,
                        stream, a);
     return hipGetLastError();
 }
 
 template <int MR>
 hipError_t launch_gemv_m(const W8A16Args& a, hipStream_t stream) {
-    const int64_t cpl = (a.width / 16 + 255) / 256;
-    switch (cpl) {
-        case 1: return launch_gemv_cfg<MR, 1, 8, true>(a, stream);
-        case 2: return launch_gemv_cfg<MR, 2, 4, true>(a, stream);
-        case 3: return launch_gemv_cfg<MR, 3, 4, MR < 4>(a, stream);
-        default: return launch_gemv_cfg<MR, 4, 4, MR < 4>(a, stream);
+    switch (gemv_cfg_override()) {
+        case 11: return launch_gemv_cfg<MR, 1, 1>(a, stream);
+        case 12: return launch_gemv_cfg<MR, 1, 2>(a, stream);
+        case 14: return launch_gemv_cfg<MR, 1, 4>(a, stream);
+        case 18: return launch_gemv_cfg<MR, 1, 8>(a, stream);
+        case 21: return launch_gemv_cfg<MR, 2, 1>(a, stream);
+        case 22: return launch_gemv_cfg<MR, 2, 2>(a, stream);
+        case 24: return launch_gemv_cfg<MR, 2, 4>(a, stream);
+        default: break;
     }
+    // Measured on MI355X over the BASELINE decode shapes: 64 bytes of weights
+    // in flight per lane (128 with four activation rows), two chunks per
+    // lane once a row is wider than 512 chunks, and more, smaller
+    // workgroups when the whole matrix is a few MB.
+    const int64_t chunks = a.width / 16;
+    if (a.columns * a.width <= (4 << 20)) return launch_gemv_cfg<MR, 2, 1>(a, stream);
+    if (chunks > 512) return launch_gemv_cfg<MR, 2, 4>(a, stream);
+    if (MR == 4) return launch_gemv_cfg<MR, 1, 8>(a, stream);
+    return launch_gemv_cfg<MR, 1, 4>(a, stream);
 }
 
 // ---------------------------------------------------------------------------

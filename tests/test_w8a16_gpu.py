@@ -64,6 +64,21 @@ def test_gemv_small_and_odd_shapes(oracle, rows, width, columns):
     assert tolerance.rel_err(got, route.astype(np.float64)) <= tolerance.FP16_REL_TOL
 
 
+@pytest.mark.parametrize("cfg", ["11", "12", "14", "18", "21", "22", "24"])
+def test_gemv_every_configuration(oracle, monkeypatch, cfg):
+    # OMNI_W8A16_GEMV pins one GEMV instantiation (chunks per lane, rows per
+    # workgroup); each must agree with the oracle on ragged shapes, including
+    # the widest row (16384) and a row narrower than one wavefront of chunks.
+    monkeypatch.setenv("OMNI_W8A16_GEMV", cfg)
+    for rows, width, columns in ((1, 4096, 77), (4, 16384, 9), (3, 1536, 130), (2, 16, 5),
+                                 (1, 14336, 31)):
+        rng = np.random.default_rng(rows + width + columns + int(cfg))
+        x, w, s, b = make(rng, rows, width, columns, bias=rows % 2 == 1)
+        got = host(oi.w8a16_linear(dev(x), dev(w), dev(s), None if b is None else dev(b)))
+        ref = oracle.w8a16_f64(x, w, s, b)
+        assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL, (cfg, rows, width, columns)
+
+
 def test_gemv_exact_on_integer_inputs():
     # integer x, scale 1: every partial sum is an integer below 2^11 -> exact
     x = np.tile(np.arange(-4, 4, dtype=np.float16), (4, 64))[:, :512].copy()
