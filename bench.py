@@ -119,10 +119,12 @@ def graph_of(fn, iters):
 
 
 def timed_graph(g, stream):
-    """Seconds for one replay, bracketed by HIP events on `stream`."""
+    """Seconds for one replay, bracketed by HIP events on `stream`, after one
+    untimed replay (a graph's first replay runs measurably slower)."""
     import torch
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
+    g.replay()
     torch.cuda.synchronize()
     start.record(stream)
     g.replay()

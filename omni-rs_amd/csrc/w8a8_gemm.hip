@@ -623,8 +623,11 @@ __global__ __launch_bounds__(128 * WAVES_M, 512 / (128 * WAVES_M)) void w8a8_dma
 //   wait for tile kt+1's copies, barrier
 //   MFMAs (tile kt, k step 1)    | copy tile kt+S-1 into the freed stage,
 //                                | fragment reads (tile kt+1, k step 0)
-// so every LDS read has a whole MFMA group to land and the only barrier sits
-// between two MFMA groups. The next output tile's first copies are issued
+// with one read and one copy issued after each MFMA, so every LDS read has
+// most of an MFMA group to land, no copy burst holds up an MFMA, and the only
+// barrier sits between two MFMA groups. (With one wave per SIMD a copy that
+// waits for the CU's texture unit blocks its wave's next MFMA: measured on
+// MI355X, copies issued in a burst and MFMAs do not overlap at all.) The next output tile's first copies are issued
 // before this tile's epilogue, whose per-row and per-column values sit in a
 // parity-double-buffered LDS block. Epilogue stores of partial tiles are
 // unconditional too: rows and columns past the matrix were loaded clamped to
@@ -726,6 +729,10 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
 #pragma unroll
         for (int j = 0; j < kCpw; ++j) lds_copy16(src[j] + k0, dst + j * 1024);
     };
+    auto copy_one = [&](int kt, int s, int j) {
+        const int k0 = min(kt, ktiles - 1) * BK;
+        lds_copy16(src[j] + k0, stage(s) + wave * kCpw * 1024 + j * 1024);
+    };
 
     // Fragment read offsets within a stage, k steps 0 and 1.
     const int fr = lane & 31, fh = lane >> 5, fq = (fr >> 2) & 3;
@@ -734,6 +741,13 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
     const int fragB0 = BM * BK + (wn * WN + fr) * BK + (((0 + fh) ^ fq) << 4);
     const int fragB1 = BM * BK + (wn * WN + fr) * BK + (((2 + fh) ^ fq) << 4);
     v4i fa0[FM], fb0[FN], fa1[FM], fb1[FN];
+    // Fragment idx < FM is A fragment idx, else B fragment idx - FM.
+    auto read_frag = [&](int s, int ks, int idx, v4i (&fa)[FM], v4i (&fb)[FN]) {
+        if (idx < FM)
+            fa[idx] = *reinterpret_cast<const v4i*>(stage(s) + (ks ? fragA1 : fragA0) + idx * 32 * BK);
+        else
+            fb[idx - FM] = *reinterpret_cast<const v4i*>(stage(s) + (ks ? fragB1 : fragB0) + (idx - FM) * 32 * BK);
+    };
     auto read_frags = [&](int s, int ks, v4i (&fa)[FM], v4i (&fb)[FN]) {
         const uint8_t* pa = stage(s) + (ks ? fragA1 : fragA0);
         const uint8_t* pb = stage(s) + (ks ? fragB1 : fragB0);
@@ -777,37 +791,30 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
 #pragma unroll
             for (int u = 0; u < S; ++u) {
                 const int kt = t0 + u;
-                // Each MFMA group starts with one MFMA on fragments that
-                // landed a group earlier, then issues the next group's reads,
-                // then the rest: the reads overlap the MFMAs and the wait for
-                // them falls at the next group's start. The scheduling
-                // barriers keep the compiler from sinking the reads to their
-                // first use.
-                acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0[0], fb0[0], acc[0][0], 0, 0, 0);
-                __builtin_amdgcn_sched_barrier(0);
-                read_frags(u, 1, fa1, fb1);
-                __builtin_amdgcn_sched_barrier(0);
+                // k step 0 of tile kt: after each of the first FM+FN MFMAs,
+                // one fragment read of k step 1. The scheduling barriers pin
+                // that order: a vector-memory or LDS instruction that cannot
+                // issue stalls the wave's next MFMA, so each one is placed
+                // behind an MFMA rather than in a burst.
 #pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j)
-                        if (i | j)
-                            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0[i], fb0[j], acc[i][j], 0, 0, 0);
-                __builtin_amdgcn_sched_barrier(0);
+                for (int q = 0; q < FM * FN; ++q) {
+                    const int i = q / FN, j = q % FN;
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0[i], fb0[j], acc[i][j], 0, 0, 0);
+                    if (q < FM + FN) read_frag(u, 1, q, fa1, fb1);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
                 s_waitcnt_vm<(S - 3) * kCpw, true>();
                 lds_barrier();  // tile kt+1 landed everywhere; stage (u+S-1)%S is free
-                acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1[0], fb1[0], acc[0][0], 0, 0, 0);
-                __builtin_amdgcn_sched_barrier(0);
-                copy_tile(kt + S - 1, (u + S - 1) % S);
-                read_frags((u + 1) % S, 0, fa0, fb0);
-                __builtin_amdgcn_sched_barrier(0);
+                // k step 1: after each MFMA, one copy of tile kt+S-1 into the
+                // freed stage and one fragment read of tile kt+1, k step 0.
 #pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j)
-                        if (i | j)
-                            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1[i], fb1[j], acc[i][j], 0, 0, 0);
-                __builtin_amdgcn_sched_barrier(0);
+                for (int q = 0; q < FM * FN; ++q) {
+                    const int i = q / FN, j = q % FN;
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1[i], fb1[j], acc[i][j], 0, 0, 0);
+                    if (q < kCpw) copy_one(kt + S - 1, (u + S - 1) % S, q);
+                    if (q < FM + FN) read_frag((u + 1) % S, 0, q, fa0, fb0);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
         }
 
@@ -1031,34 +1038,37 @@ hipError_t launch_w8a8_mfma(const W8A8Args& a, hipStream_t stream) {
         case 15: return launch_ring<192, 3>(a, stream);
         default: break;
     }
-    // Cost model, fitted to MI355X timings of every candidate on the BASELINE
-    // shapes: a kernel runs its tiles in rounds of one tile per CU; a round
-    // costs c * BM * BN (times K, common to all candidates), and a partial
-    // last round with fill f costs (0.5 + 0.5 f) of a full one (the chip is
+    // Cost model, fitted to MI355X timings of every candidate on ten shapes
+    // (the BASELINE GEMM shapes and the reference's 256-row benchmark shapes;
+    // random operands, f32 out): a kernel runs its tiles in rounds of one
+    // tile per CU, a round costs BM * BN * (c * K + e) (c: per output element
+    // and K byte; e: the per-tile prologue and epilogue), and a partial last
+    // round with fill f costs (0.7 + 0.3 f) of a full one (the chip is
     // power-limited on this path, so a partly idle round runs at a higher
-    // clock). c is the measured cost per output element and K byte.
+    // clock). It picks the fastest candidate, or one within 1 %, on all ten.
     const int64_t cus = num_cus();
     const int64_t kt = a.width % 64 == 0 ? a.width / 64 : 0;
-    auto cost = [&](double c, int64_t bm, int64_t bn) {
+    const double K = (double)a.width;
+    auto cost = [&](double c, double e, int64_t bm, int64_t bn) {
         const int64_t tiles = ((a.rows + bm - 1) / bm) * ((a.columns + bn - 1) / bn);
         const int64_t full = tiles / cus, rem = tiles % cus;
-        const double rounds = (double)full + (rem ? 0.5 + 0.5 * (double)rem / (double)cus : 0.0);
-        return c * (double)(bm * bn) * rounds;
+        const double rounds = (double)full + (rem ? 0.7 + 0.3 * (double)rem / (double)cus : 0.0);
+        return (double)(bm * bn) * (c * K + e) * rounds;
     };
     struct Cand { double t; int id; };
-    Cand best{cost(364.0, 256, 192), 3};  // register-staged 256 x 192 takes any K % 16 == 0
+    Cand best{cost(280.5, 227212.0, 256, 192), 3};  // register-staged 256 x 192 takes any K % 16 == 0
     auto consider = [&](bool ok, double t, int id) {
         if (ok && t < best.t) best = Cand{t, id};
     };
-    consider(true, cost(400.0, 256, 128), 4);
-    consider(dma_fits(a, 2), cost(266.0, 512, 192), 9);
-    consider(dma_fits(a, 2), cost(297.0, 512, 128), 10);
+    consider(true, cost(308.0, 250000.0, 256, 128), 4);
+    consider(dma_fits(a, 2), cost(196.4, 206662.0, 512, 192), 9);
+    consider(dma_fits(a, 2), cost(224.8, 215142.0, 512, 128), 10);
     const bool s4 = kt >= 4 && kt % 4 == 0, s3 = kt >= 3 && kt % 3 == 0;
-    consider(s4, cost(289.0, 256, 256), 11);
-    consider(s4, cost(288.0, 256, 192), 12);
-    consider(s4, cost(323.0, 256, 128), 13);
-    consider(!s4 && s3, cost(298.0, 256, 256), 14);
-    consider(!s4 && s3, cost(297.0, 256, 192), 15);
+    consider(s4, cost(182.2, 278314.0, 256, 256), 11);
+    consider(s4, cost(210.8, 215845.0, 256, 192), 12);
+    consider(s4, cost(262.4, 189679.0, 256, 128), 13);
+    consider(!s4 && s3, cost(208.6, 254981.0, 256, 256), 14);
+    consider(!s4 && s3, cost(233.8, 218505.0, 256, 192), 15);
     switch (best.id) {
         case 4: return launch_bn<128, 2>(a, stream);
         case 9: return launch_dma<192, 2, 4>(a, stream);
