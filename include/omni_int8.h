@@ -117,6 +117,37 @@ int omni_try_int8_gemm(const void* x, int x_dtype, int64_t rows, int64_t width,
                        int64_t scale_len, const int32_t* w_zero, int64_t zero_len, float* out,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/* ConvRot activation rotation fused into per-row quantisation.
+ * Replaces the rotate step of Int8Linear::forward followed by
+ * try_int8_gemm's quantize_rows: crates/qwen-image/src/convrot.rs:86-88 and
+ * :113-119 (rotate), the matrix of :121-149 (hadamard, sign_negative), then
+ * crates/omni-kernel/src/int8_matmul.rs:23-118.
+ *   r = each group of 256 consecutive elements of a row times H,
+ *   H = 2^-4 * H4 (x) H4 (x) H4 (x) H4 with H4[a][b] = -1 iff a ^ b == 3;
+ *   then codes, row scales and row sums of r as omni_int8_quantize_rows.
+ * r is computed in f32 by a fast transform, not by a 256-term dot: its
+ * rounding differs from the reference's f32 matmul by a few ulp, so a code
+ * can differ by one where r / row_scale lies within that of k + 0.5.
+ * group must be 256 (convrot.rs:12), width % 256 == 0 (convrot.rs:39-43),
+ * else OMNI_NOT_HANDLED; x and every row start (ld_x) 16-byte aligned,
+ * x_packed 8-byte aligned. x_sum may be NULL. */
+int omni_convrot_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t width,
+                               int64_t ld_x, int64_t group, int32_t* x_packed, float* x_scale,
+                               int32_t* x_sum, void* stream);
+
+/* The whole ConvRot linear layer: rotation + quantisation + W8A8 GEMM, output
+ * in the model precision. Replaces Int8Linear::forward with project,
+ * crates/qwen-image/src/convrot.rs:81-102. Shape guard as omni_try_int8_gemm
+ * (columns = scale_len) plus width % 256 == 0; OMNI_NOT_HANDLED where the
+ * reference panics. out_dtype OMNI_F16 (the model's Precision::F16: the f32
+ * result rounded once to nearest even, convrot.rs:91) or OMNI_F32.
+ * x contiguous [rows][width]; workspace as omni_try_int8_gemm
+ * (omni_try_int8_gemm_workspace_size(rows, width) bytes, 256-byte aligned). */
+int omni_convrot_linear(const void* x, int x_dtype, int64_t rows, int64_t width,
+                        const int32_t* w_packed, int64_t w_packed_len, const float* w_scale,
+                        int64_t scale_len, const int32_t* w_zero, int64_t zero_len, void* out,
+                        int out_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Weight-only int8 linear with fp16 per-output-channel scales (W8A16).
  * No single counterpart in the reference: it follows the reference's
  * dequantisation convention, w_deq = w * scale, f32 accumulation

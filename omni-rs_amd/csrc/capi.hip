@@ -205,6 +205,78 @@ int omni_try_int8_gemm(const void* x, int x_dtype, int64_t rows, int64_t width,
                           columns, width, out, OMNI_F32, nullptr, OMNI_LOWERING_AUTO, stream);
 }
 
+int omni_convrot_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t width,
+                               int64_t ld_x, int64_t group, int32_t* x_packed, float* x_scale,
+                               int32_t* x_sum, void* stream) {
+    if (rows < 0 || width < 0 || ld_x < width)
+        return fail(OMNI_BAD_ARGUMENT, "convrot_quantize_rows: bad sizes rows=%lld width=%lld ld=%lld",
+                    (long long)rows, (long long)width, (long long)ld_x);
+    if (x_dtype != OMNI_F32 && x_dtype != OMNI_F16)
+        return fail(OMNI_BAD_ARGUMENT, "convrot_quantize_rows: unknown dtype %d", x_dtype);
+    // crates/qwen-image/src/convrot.rs:12 (GROUP = 256) and :39-43 (the width
+    // must split into whole groups).
+    if (group != 256)
+        return fail(OMNI_NOT_HANDLED, "convrot_quantize_rows: group %lld (only 256 is supported)",
+                    (long long)group);
+    if (width % 256 != 0)
+        return fail(OMNI_NOT_HANDLED, "convrot_quantize_rows: width %lld is not a multiple of 256",
+                    (long long)width);
+    if (rows == 0 || width == 0) return OMNI_OK;
+    if (!x || !x_packed || !x_scale)
+        return fail(OMNI_BAD_ARGUMENT, "convrot_quantize_rows: null pointer");
+    const int64_t elem = x_dtype == OMNI_F16 ? 2 : 4;
+    if (!aligned(x, 16) || (ld_x * elem) % 16 != 0)
+        return fail(OMNI_BAD_ARGUMENT, "convrot_quantize_rows: x rows must start 16-byte aligned");
+    if (!aligned(x_packed, 8)) return fail(OMNI_BAD_ARGUMENT, "convrot_quantize_rows: x_packed misaligned");
+    if (rows > 0x7fffffffLL) return fail(OMNI_BAD_ARGUMENT, "convrot_quantize_rows: too many rows");
+    int st = check_current_device();
+    if (st != OMNI_OK) return st;
+    return hip_status(omni::launch_convrot_quantize(x, x_dtype == OMNI_F16, rows, width, ld_x,
+                                                    reinterpret_cast<uint8_t*>(x_packed), x_scale,
+                                                    x_sum, static_cast<hipStream_t>(stream)),
+                      "convrot_quantize_rows launch");
+}
+
+int omni_convrot_linear(const void* x, int x_dtype, int64_t rows, int64_t width,
+                        const int32_t* w_packed, int64_t w_packed_len, const float* w_scale,
+                        int64_t scale_len, const int32_t* w_zero, int64_t zero_len, void* out,
+                        int out_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+    // Int8Linear::forward (crates/qwen-image/src/convrot.rs:81-92): the width
+    // must match the layer (:84 asserts it), the layer's tensors must agree
+    // (try_int8_gemm's guard, int8_matmul.rs:517-521), the width must split
+    // into groups of 256 (:39-43).
+    const int64_t columns = scale_len;
+    if (rows < 0 || width < 0 || columns < 0)
+        return fail(OMNI_BAD_ARGUMENT, "convrot_linear: negative size");
+    if (width % 256 != 0 || w_packed_len != columns * width / 4 || zero_len != columns)
+        return fail(OMNI_NOT_HANDLED,
+                    "convrot_linear: shapes disagree (width=%lld packed=%lld columns=%lld zero=%lld)",
+                    (long long)width, (long long)w_packed_len, (long long)columns, (long long)zero_len);
+    if (x_dtype != OMNI_F32 && x_dtype != OMNI_F16)
+        return fail(OMNI_BAD_ARGUMENT, "convrot_linear: unknown dtype %d", x_dtype);
+    if (out_dtype != OMNI_F32 && out_dtype != OMNI_F16)
+        return fail(OMNI_BAD_ARGUMENT, "convrot_linear: unknown out dtype %d", out_dtype);
+    if (workspace_bytes < omni_try_int8_gemm_workspace_size(rows, width))
+        return fail(OMNI_BAD_ARGUMENT, "convrot_linear: workspace of %zu bytes, need %zu",
+                    workspace_bytes, omni_try_int8_gemm_workspace_size(rows, width));
+    if (rows == 0 || columns == 0) return OMNI_OK;
+    if (!x || !w_packed || !w_scale || !w_zero || !out || !workspace)
+        return fail(OMNI_BAD_ARGUMENT, "convrot_linear: null pointer");
+    if (!aligned(workspace, 256)) return fail(OMNI_BAD_ARGUMENT, "convrot_linear: workspace must be 256-byte aligned");
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    int32_t* x_packed = reinterpret_cast<int32_t*>(ws);
+    float* x_scale = reinterpret_cast<float*>(ws + round_up((size_t)rows * width, 256));
+    int32_t* x_sum = reinterpret_cast<int32_t*>(ws + round_up((size_t)rows * width, 256) +
+                                                round_up((size_t)rows * 4, 256));
+    int st = omni_convrot_quantize_rows(x, x_dtype, rows, width, width, 256, x_packed, x_scale,
+                                        x_sum, stream);
+    if (st != OMNI_OK) return st;
+    // The reference casts the f32 result to the model precision after the op
+    // (convrot.rs:91); the GEMM's f16 epilogue applies that same one rounding.
+    return omni_w8a8_gemm(x_packed, x_scale, x_sum, w_packed, w_scale, w_zero, nullptr, rows,
+                          columns, width, out, out_dtype, nullptr, OMNI_LOWERING_AUTO, stream);
+}
+
 int omni_w8a16_gemm(const uint16_t* x, const int8_t* w, const uint16_t* scale,
                     const uint16_t* bias, int64_t rows, int64_t columns, int64_t width,
                     uint16_t* out, void* stream) {

@@ -53,4 +53,49 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
     return v;
 }
 
+// RN(x / s) given y = RN(1 / s): q0 = x * y, r = fma(-q0, s, x),
+// q = fma(r, y, q0) (Markstein's correction step) returns the correctly
+// rounded quotient whenever the residual r is exact, which holds for
+// s >= 2^-90; TINY rows (s below that) use the IEEE division itself.
+template <bool TINY>
+__device__ __forceinline__ float div_rn(float x, float s, float y) {
+#pragma clang fp contract(off)
+    if constexpr (TINY) return x / s;
+    const float q0 = x * y;
+    const float r = __builtin_fmaf(-q0, s, x);
+    return __builtin_fmaf(r, y, q0);
+}
+
+// Codes of four consecutive values packed little-endian into one word; the
+// codes' sum is accumulated with one v_dot4 against 1,1,1,1.
+//
+// Rounding: trunc(q + copysign(0.5, q)) equals sign(q) * floor(|q| + 0.5)
+// with the same f32 addition as the reference (q - 0.5 is exactly
+// -(|q| + 0.5)), and v_cvt_i32_f32 truncates toward zero and maps NaN to 0.
+// |q| <= 127 * (1 + 2^-23) always (the row scale is the peak / 127), so the
+// clamp to [-128, 127] only ever matters for NaN/Inf-derived values.
+template <bool TINY>
+__device__ __forceinline__ u32 pack4(const float* v, float s, float y, int& sum) {
+    int c[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const float q = div_rn<TINY>(v[b], s, y);
+        const int r = (int)(q + __builtin_copysignf(0.5f, q));
+        c[b] = r < -128 ? -128 : (r > 127 ? 127 : r);
+    }
+    const u32 lo = __builtin_amdgcn_perm((u32)c[1], (u32)c[0], 0x0c0c0400u);  // c0.b0, c1.b0
+    const u32 hi = __builtin_amdgcn_perm((u32)c[3], (u32)c[2], 0x0c0c0400u);  // c2.b0, c3.b0
+    const u32 word = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+    sum = __builtin_amdgcn_sdot4((int)word, 0x01010101, sum, false);
+    return word;
+}
+
+// Row scale from the peak: max(peak / 127, 1e-30) (int8_matmul.rs:63-68).
+__device__ __forceinline__ float row_scale_of(float peak) {
+    float row_scale = peak / 127.0f;
+    // `!(a > b)` also catches a NaN peak, like Rust's f32::max with 1e-30.
+    if (!(row_scale > 1.0e-30f)) row_scale = 1.0e-30f;
+    return row_scale;
+}
+
 }  // namespace omni

@@ -10,6 +10,12 @@ hipError_t launch_quantize_rows(const void* x, bool x_is_f16, int64_t rows, int6
                                 int64_t ld, uint8_t* codes, float* scale, int32_t* sum,
                                 hipStream_t stream);
 
+// ConvRot group-256 Hadamard rotation fused into quantize_rows (convrot.hip);
+// width % 256 == 0, x and every row start 16-byte aligned.
+hipError_t launch_convrot_quantize(const void* x, bool x_is_f16, int64_t rows, int64_t width,
+                                   int64_t ld, uint8_t* codes, float* scale, int32_t* sum,
+                                   hipStream_t stream);
+
 struct W8A8Args {
     const uint8_t* x;      // [rows][width] int8 codes
     const float* x_scale;  // [rows]
