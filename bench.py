@@ -184,6 +184,51 @@ def cpu_gemv_baseline(oracle, np, seconds):
                       f"{elapsed:.1f} s single-thread C restatement"}
 
 
+def convrot_bench(torch, oi, gen, dev, stream, steps):
+    """BASELINE config 4 (M=4352 = 4096 image + 256 text tokens): the fused
+    ConvRot rotation + quantisation of the f16 activations at widths 3072
+    (QKV / MLP-up input) and 12288 (MLP-down input), in HBM GB/s of its
+    algorithmic bytes (2 B read + 1 B code written per element, 8 B per row),
+    and one whole Int8Linear layer (QKV, N=9216, f16 out) in TOPS."""
+    from omni_int8 import convrot
+    M = 4352
+    res = {"config": "BASELINE config 4, M=4352, f16 activations ~ N(0,1)"}
+    kernels = []
+    for K in (3072, 12288):
+        x = torch.randn((M, K), generator=gen, device=dev).half()
+
+        def fused(x=x):
+            convrot.convrot_quantize_rows(x)
+
+        for _ in range(3):
+            fused()
+        g = graph_of(fused, steps)
+        t = timed_graph(g, stream) / steps
+        del g
+        nbytes = 3 * M * K + 8 * M
+        kernels.append({"M": M, "K": K, "us": round(t * 1e6, 2), "GB/s": round(nbytes / t / 1e9, 1),
+                        "roofline_frac": round(nbytes / t / 1e9 / PEAK_HBM_GBS, 4)})
+    res["rotate_quantize"] = kernels
+    K, N = 3072, 9216
+    x = torch.randn((M, K), generator=gen, device=dev).half()
+    w = torch.randint(-127, 128, (N, K), generator=gen, device=dev, dtype=torch.int8)
+    layer = convrot.Int8Linear(K, N, w.view(torch.int32).reshape(-1),
+                               torch.rand(N, generator=gen, device=dev) * 0.018 + 0.002,
+                               torch.zeros(N, dtype=torch.int32, device=dev))
+
+    def lin():
+        layer(x)
+
+    for _ in range(3):
+        lin()
+    g = graph_of(lin, steps)
+    t = timed_graph(g, stream) / steps
+    del g
+    res["layer"] = {"M": M, "K": K, "N": N, "out": "f16", "us": round(t * 1e6, 2),
+                    "tops": round(2.0 * M * N * K / t / 1e12, 1)}
+    return res
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -281,6 +326,9 @@ def main():
     gemv_bytes = gN * gK + 2 * gN + 2 * gM * gK + 2 * gM * gN
     gemv_gbs = gemv_bytes / t_gemv / 1e9
 
+    # ---- ConvRot: fused rotation + quantisation, and one whole layer ---------
+    convrot_res = convrot_bench(torch, oi, gen, dev, stream, args.steps)
+
     # ---- CPU baselines (oracle, bounded samples) -----------------------------
     import oracle_lib
     oracle = oracle_lib.Oracle()
@@ -318,6 +366,7 @@ def main():
                          "traffic": traffic.get("w8a16_gemv")},
             "cpu_baseline": cpu_gemv,
         },
+        "convrot": convrot_res,
     }
     print(json.dumps(line))
 

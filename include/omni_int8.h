@@ -130,7 +130,7 @@ int omni_try_int8_gemm(const void* x, int x_dtype, int64_t rows, int64_t width,
  * can differ by one where r / row_scale lies within that of k + 0.5.
  * group must be 256 (convrot.rs:12), width % 256 == 0 (convrot.rs:39-43),
  * else OMNI_NOT_HANDLED; x and every row start (ld_x) 16-byte aligned,
- * x_packed 8-byte aligned. x_sum may be NULL. */
+ * x_packed 16-byte aligned. x_sum may be NULL. */
 int omni_convrot_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t width,
                                int64_t ld_x, int64_t group, int32_t* x_packed, float* x_scale,
                                int32_t* x_sum, void* stream);

@@ -227,7 +227,7 @@ int omni_convrot_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t
     const int64_t elem = x_dtype == OMNI_F16 ? 2 : 4;
     if (!aligned(x, 16) || (ld_x * elem) % 16 != 0)
         return fail(OMNI_BAD_ARGUMENT, "convrot_quantize_rows: x rows must start 16-byte aligned");
-    if (!aligned(x_packed, 8)) return fail(OMNI_BAD_ARGUMENT, "convrot_quantize_rows: x_packed misaligned");
+    if (!aligned(x_packed, 16)) return fail(OMNI_BAD_ARGUMENT, "convrot_quantize_rows: x_packed must be 16-byte aligned");
     if (rows > 0x7fffffffLL) return fail(OMNI_BAD_ARGUMENT, "convrot_quantize_rows: too many rows");
     int st = check_current_device();
     if (st != OMNI_OK) return st;
