@@ -45,6 +45,13 @@ __device__ __forceinline__ float w8a8_epilogue(int acc, int sum, int zero, float
     return v;
 }
 
+// Output stores of the MFMA kernels: the output is written once and read by
+// the next operator, not by this kernel, so it is stored nontemporally.
+template <typename T>
+__device__ __forceinline__ void stream_store(T* p, T v) {
+    __builtin_nontemporal_store(v, p);
+}
+
 __device__ __forceinline__ void store_out(void* out, int64_t idx, float v, bool out_f16) {
     if (out_f16)
         static_cast<_Float16*>(out)[idx] = (_Float16)v;  // v_cvt_f16_f32: round to nearest even
@@ -599,9 +606,9 @@ __global__ __launch_bounds__(128 * WAVES_M, 512 / (128 * WAVES_M)) void w8a8_dma
                     if (full || (lr0 + dr < rows_left && lc < cols_left)) {
                         if constexpr (DUMP) a.acc_dump[tile_base + off] = v;
                         if constexpr (OUT16)
-                            static_cast<_Float16*>(a.out)[tile_base + off] = (_Float16)o;
+                            stream_store(static_cast<_Float16*>(a.out) + tile_base + off, (_Float16)o);
                         else
-                            static_cast<float*>(a.out)[tile_base + off] = o;
+                            stream_store(static_cast<float*>(a.out) + tile_base + off, o);
                     }
                 }
             }
@@ -880,9 +887,9 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
                             const float o = w8a8_epilogue(v, rsum[e], zero, rs[e], ws, bias, has_bias);
                             if constexpr (DUMP) dump[off] = v;
                             if constexpr (OUT16)
-                                out16[off] = (_Float16)o;
+                                stream_store(out16 + off, (_Float16)o);
                             else
-                                out32[off] = o;
+                                stream_store(out32 + off, o);
                         }
                     }
                     __builtin_amdgcn_sched_barrier(0);
