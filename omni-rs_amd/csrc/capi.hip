@@ -74,6 +74,13 @@ bool force_scalar() {
 
 bool aligned(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
 
+// OMNI_W8A16_ROUTE=2 sends 5..64-row W8A16 calls to the tiled MFMA GEMM
+// instead of the skinny kernel (test aid; read on every call).
+int w8a16_route() {
+    const char* v = std::getenv("OMNI_W8A16_ROUTE");
+    return v ? std::atoi(v) : 0;
+}
+
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 int run_w8a8(const int32_t* x_packed, const float* x_scale, const int32_t* x_sum,
@@ -305,6 +312,9 @@ int omni_w8a16_gemm(const uint16_t* x, const int8_t* w, const uint16_t* scale,
     // 16-element chunk per lane: width <= 16384.
     if (rows <= 4 && width <= 16384)
         return hip_status(omni::launch_w8a16_gemv(a, s), "w8a16 gemv launch");
+    // 5..64 rows: the weights are streamed once by a GEMV-shaped MFMA kernel.
+    if (rows <= 64 && w8a16_route() != 2)
+        return hip_status(omni::launch_w8a16_skinny(a, s), "w8a16 skinny launch");
     return hip_status(omni::launch_w8a16_mfma(a, s), "w8a16 mfma launch");
 }
 

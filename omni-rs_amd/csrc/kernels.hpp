@@ -43,6 +43,7 @@ struct W8A16Args {
 };
 
 hipError_t launch_w8a16_gemv(const W8A16Args& a, hipStream_t stream);
+hipError_t launch_w8a16_skinny(const W8A16Args& a, hipStream_t stream);
 hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream);
 
 }  // namespace omni

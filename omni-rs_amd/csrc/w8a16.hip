@@ -233,6 +233,109 @@ hipError_t launch_gemv_m(const W8A16Args& a, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------
+// Skinny GEMM (5..64 activation rows): GEMV-shaped, on fp16 MFMA.
+// ---------------------------------------------------------------------------
+
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+
+// MB blocks of 16 activation rows. A 1024-lane workgroup owns 16 weight rows
+// (output columns) n0..n0+15 and splits K over its 16 waves in steps of 64
+// (wave w takes steps w, w + 16, ...). Per step a lane loads 16 weight codes
+// (row n0 + lane % 16, k = k0 + 16 (lane / 16) .. +16) and the same 16 k of
+// activation row lane % 16 of each block, and feeds two
+// v_mfma_f32_16x16x32_f16: the first on codes 0..7 of every lane, the second
+// on codes 8..15. Within one MFMA the hardware's k order is its own, but A and
+// B use the same lane-to-k map, so each product pairs matching k and the 64
+// k of the step are summed exactly once. The 16 waves' 16 x 16 partial tiles
+// are reduced through LDS; scale (and bias) are applied once per output.
+template <int MB>
+__global__ __launch_bounds__(1024) void w8a16_skinny_kernel(W8A16Args a) {
+    __shared__ float s_part[16][MB][256];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int64_t K = a.width;
+    const int64_t n0 = (int64_t)blockIdx.x * 16;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int64_t wn = n0 + r16 < a.columns ? n0 + r16 : a.columns - 1;  // clamped: never stored
+    const int8_t* wrow = a.w + wn * K;
+    const _Float16* xrow[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+        const int64_t m = mb * 16 + r16 < a.rows ? mb * 16 + r16 : a.rows - 1;  // clamped: never stored
+        xrow[mb] = a.x + m * K;
+    }
+    v4f_t acc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
+    const int64_t steps = (K + 63) / 64;
+    auto step = [&](int64_t st) {
+        const int64_t k = st * 64 + 16 * g;
+        typedef unsigned v4u __attribute__((ext_vector_type(4)));
+        v4u wv = v4u{0u, 0u, 0u, 0u};
+        uint4 xv[MB][2];
+        // K % 16 == 0: a lane's 16-element block is wholly inside or outside.
+        if (k < K) {
+            wv = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wrow + k));
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                xv[mb][0] = reinterpret_cast<const uint4*>(xrow[mb] + k)[0];
+                xv[mb][1] = reinterpret_cast<const uint4*>(xrow[mb] + k)[1];
+            }
+        } else {
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) xv[mb][0] = xv[mb][1] = make_uint4(0, 0, 0, 0);
+        }
+        v2h h[8];
+        i8x4_to_f16x4(wv.x, h[0], h[1]);
+        i8x4_to_f16x4(wv.y, h[2], h[3]);
+        i8x4_to_f16x4(wv.z, h[4], h[5]);
+        i8x4_to_f16x4(wv.w, h[6], h[7]);
+        const v8h b0 = {h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
+        const v8h b1 = {h[4][0], h[4][1], h[5][0], h[5][1], h[6][0], h[6][1], h[7][0], h[7][1]};
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+            v8h a0, a1;
+            __builtin_memcpy(&a0, &xv[mb][0], 16);
+            __builtin_memcpy(&a1, &xv[mb][1], 16);
+            acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b0, acc[mb], 0, 0, 0);
+            acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b1, acc[mb], 0, 0, 0);
+        }
+    };
+    int64_t st = wave;
+    for (; st + 16 < steps; st += 32) {  // two steps per trip: their loads overlap
+        step(st);
+        step(st + 16);
+    }
+    if (st < steps) step(st);
+    // 16 x 16 accumulator layout: lane holds column lane % 16, rows
+    // 4 (lane / 16) .. +3.
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s_part[wave][mb][(4 * g + r) * 16 + r16] = acc[mb][r];
+    __syncthreads();
+    if (tid < MB * 256) {
+        const int mb = tid >> 8, e = tid & 255;
+        const int64_t m = mb * 16 + (e >> 4), n = n0 + (e & 15);
+        if (m < a.rows && n < a.columns) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 16; ++w) sum += s_part[w][mb][e];
+            const float bi = a.bias ? (float)a.bias[n] : 0.0f;
+            a.out[m * a.columns + n] = (_Float16)(sum * (float)a.scale[n] + bi);
+        }
+    }
+}
+
+template <int MB>
+hipError_t launch_skinny_cfg(const W8A16Args& a, hipStream_t stream) {
+    const int64_t grid = (a.columns + 15) / 16;
+    hipLaunchKernelGGL((w8a16_skinny_kernel<MB>), dim3((unsigned)grid), dim3(1024), 0, stream, a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // Prefill GEMM on fp16 MFMA.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int xcd_remap16(int b, int total) {
@@ -401,6 +504,14 @@ hipError_t launch_w8a16_gemv(const W8A16Args& a, hipStream_t stream) {
         case 2: return launch_gemv_m<2>(a, stream);
         default: return launch_gemv_m<4>(a, stream);  // 3 rows run with one zero row
     }
+}
+
+hipError_t launch_w8a16_skinny(const W8A16Args& a, hipStream_t stream) {
+    if (a.rows == 0 || a.columns == 0) return hipSuccess;
+    if (a.rows <= 16) return launch_skinny_cfg<1>(a, stream);
+    if (a.rows <= 32) return launch_skinny_cfg<2>(a, stream);
+    if (a.rows <= 48) return launch_skinny_cfg<3>(a, stream);
+    return launch_skinny_cfg<4>(a, stream);
 }
 
 hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream) {

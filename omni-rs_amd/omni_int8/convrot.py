@@ -9,7 +9,9 @@ whole layer is one C-ABI call (``omni_convrot_linear``).
 """
 from __future__ import annotations
 
-from typing import Optional
+import json
+import os
+from typing import Dict, Optional, Tuple
 
 import numpy as np
 import torch
@@ -18,6 +20,116 @@ from . import _lib
 from ._lib import OMNI_F16, OMNI_F32, OMNI_NOT_HANDLED
 
 GROUP = 256  # crates/qwen-image/src/convrot.rs:12
+FILE_NAME = "Qwen-Image-2.1-Turbo-INT8-ConvRot.safetensors"  # convrot.rs:13
+
+
+class CheckpointError(ValueError):
+    """A malformed checkpoint, a missing tensor or one of the wrong dtype
+    (the reference's Error::Checkpoint, src/weights.rs:316-320, 429-462)."""
+
+
+class ConfigError(ValueError):
+    """A layer whose tensors do not fit its declared shape (the reference's
+    Error::Config, crates/qwen-image/src/convrot.rs:39-50)."""
+
+
+# safetensors dtype tag -> numpy dtype (little-endian payloads)
+_DTYPES = {"I8": np.int8, "U8": np.uint8, "I16": np.int16, "I32": np.int32, "I64": np.int64,
+           "F16": np.float16, "BF16": np.uint16, "F32": np.float32, "F64": np.float64,
+           "BOOL": np.bool_}
+
+
+class SafetensorsFile:
+    """Read-only memory map of one safetensors file: an 8-byte little-endian
+    header length, a JSON header naming each tensor's dtype, shape and byte
+    range, then the payload. Mirrors the raw accessors of src/weights.rs
+    (open_file :301-304, raw_i8 :429-442, raw_f32 :444-462): host views of
+    one tensor, checked for dtype and length."""
+
+    def __init__(self, path: str):
+        self.path = path
+        self._map = np.memmap(path, dtype=np.uint8, mode="r")
+        if self._map.size < 8:
+            raise CheckpointError(f"{path}: too short for a safetensors header")
+        n = int(self._map[:8].view("<u8")[0])
+        if n > self._map.size - 8:
+            raise CheckpointError(f"{path}: header length {n} exceeds the file")
+        try:
+            header = json.loads(bytes(self._map[8:8 + n]).decode("utf-8"))
+        except (UnicodeDecodeError, json.JSONDecodeError) as e:
+            raise CheckpointError(f"{path}: bad header: {e}") from None
+        self._base = 8 + n
+        self.metadata = header.pop("__metadata__", {})
+        self._entries: Dict[str, Tuple[str, Tuple[int, ...], int, int]] = {}
+        for name, e in header.items():
+            try:
+                dtype, shape, (begin, end) = e["dtype"], tuple(int(d) for d in e["shape"]), e["data_offsets"]
+            except (KeyError, TypeError, ValueError):
+                raise CheckpointError(f"{path}: bad header entry for {name}") from None
+            if not (0 <= begin <= end <= self._map.size - self._base):
+                raise CheckpointError(f"{path}: {name} lies outside the file")
+            self._entries[name] = (dtype, shape, int(begin), int(end))
+
+    def names(self):
+        return sorted(self._entries)
+
+    def __contains__(self, name: str) -> bool:
+        return name in self._entries
+
+    def _view(self, name: str, want: str) -> Tuple[Tuple[int, ...], np.ndarray]:
+        if name not in self._entries:
+            raise CheckpointError(f"missing tensor {name}")
+        dtype, shape, begin, end = self._entries[name]
+        if dtype != want:
+            raise CheckpointError(f"{name}: expected {want}, got {dtype}")
+        np_dtype = np.dtype(_DTYPES[want]).newbyteorder("<")
+        count = int(np.prod(shape)) if shape else 1
+        if end - begin != count * np_dtype.itemsize:
+            raise CheckpointError(f"{name}: payload of {end - begin} bytes for shape {list(shape)}")
+        data = self._map[self._base + begin:self._base + end].view(np_dtype)
+        return shape, data
+
+    def raw_i8(self, name: str) -> Tuple[Tuple[int, ...], np.ndarray]:
+        """(shape, flat int8 view) of one I8 tensor (weights.rs:429-442)."""
+        return self._view(name, "I8")
+
+    def raw_f32(self, name: str) -> Tuple[Tuple[int, ...], np.ndarray]:
+        """(shape, flat f32 view) of one F32 tensor, any rank (weights.rs:444-462)."""
+        return self._view(name, "F32")
+
+
+class ConvRotFile:
+    """The INT8-ConvRot checkpoint of Qwen-Image-2.1-Turbo (convrot.rs:15-68)."""
+
+    def __init__(self, weights: SafetensorsFile):
+        self.weights = weights
+
+    @staticmethod
+    def open(root: str) -> Optional["ConvRotFile"]:
+        """None when the directory holds no ConvRot file (convrot.rs:20-28)."""
+        path = os.path.join(root, FILE_NAME)
+        if not os.path.isfile(path):
+            return None
+        return ConvRotFile(SafetensorsFile(path))
+
+    def linear(self, name: str, input: int, output: int, precision: torch.dtype = torch.float16,
+               device="cuda") -> "Int8Linear":
+        """One projection: ``{name}._weight_qdata`` I8 [output, input],
+        ``{name}._weight_scale`` F32 [output], ``{name}._weight_zero_point`` I8
+        [output] (convrot.rs:30-67). The int8 rows go to the device as they
+        are: their bytes already are the packed words (convrot.rs:151-160)."""
+        if input % GROUP or input % 4:
+            raise ConfigError(f"{name}: ConvRot input width {input} cannot be rotated in groups of {GROUP}")
+        q_shape, codes = self.weights.raw_i8(f"{name}._weight_qdata")
+        s_shape, scale = self.weights.raw_f32(f"{name}._weight_scale")
+        z_shape, zero = self.weights.raw_i8(f"{name}._weight_zero_point")
+        if tuple(q_shape) != (output, input) or scale.size != output or zero.size != output:
+            raise ConfigError(f"{name}: ConvRot shapes {list(q_shape)} / scale {list(s_shape)} / "
+                              f"zero {list(z_shape)} do not match [{output}, {input}]")
+        # host copies out of the read-only map (raw_i8/raw_f32 copy too), then one upload each
+        packed = torch.from_numpy(np.array(codes)).to(device).view(torch.int32)
+        return Int8Linear(input, output, packed, torch.from_numpy(np.array(scale)).to(device),
+                          torch.from_numpy(zero.astype(np.int32)).to(device), precision)
 
 
 def _is_power_of_four(size: int) -> bool:

@@ -57,3 +57,86 @@ def test_layer_refuses_widths_that_do_not_split_into_groups():
     with pytest.raises(ValueError):
         convrot.Int8Linear(300, 2, torch.zeros(150, dtype=torch.int32), torch.ones(2),
                            torch.zeros(2, dtype=torch.int32))
+
+
+# -- checkpoint loader (convrot.rs:15-68, src/weights.rs:301-304, 429-462) -------
+
+def _write_layer(path, name, output, input, seed=0, scale_dtype=np.float32, extra=None):
+    from safetensors.numpy import save_file
+    rng = np.random.default_rng(seed)
+    t = {f"{name}._weight_qdata": rng.integers(-128, 128, (output, input), dtype=np.int8),
+         f"{name}._weight_scale": rng.uniform(0.002, 0.02, output).astype(scale_dtype),
+         f"{name}._weight_zero_point": rng.integers(-3, 4, output).astype(np.int8)}
+    t.update(extra or {})
+    save_file(t, path, metadata={"format": "convrot_hadamard_v1"})
+    return t
+
+
+def test_loader_reads_a_layer_written_by_the_safetensors_library(tmp_path):
+    import torch
+    name = "transformer_blocks.0.attn.to_q"
+    t = _write_layer(str(tmp_path / convrot.FILE_NAME), name, 8, 512)
+    f = convrot.ConvRotFile.open(str(tmp_path))
+    assert f is not None and f.weights.metadata["format"] == "convrot_hadamard_v1"
+    layer = f.linear(name, 512, 8, precision=torch.float16, device="cpu")
+    q = t[f"{name}._weight_qdata"]
+    assert layer.packed.dtype == torch.int32 and layer.packed.numel() == 8 * 512 // 4
+    # the packed words are the row-major int8 bytes (convrot.rs:151-160)
+    assert np.array_equal(layer.packed.numpy().view(np.int8).reshape(8, 512), q)
+    assert np.array_equal(layer.scale.numpy(), t[f"{name}._weight_scale"])
+    assert np.array_equal(layer.zero.numpy(), t[f"{name}._weight_zero_point"].astype(np.int32))
+
+
+def test_loader_raw_views_match_every_tensor(tmp_path):
+    from safetensors.numpy import save_file
+    rng = np.random.default_rng(3)
+    t = {"a": rng.integers(-128, 128, (3, 5, 7), dtype=np.int8),
+         "b": rng.standard_normal((4, 6)).astype(np.float32),
+         "c": rng.standard_normal(9).astype(np.float32)}
+    path = str(tmp_path / "x.safetensors")
+    save_file(t, path)
+    f = convrot.SafetensorsFile(path)
+    assert f.names() == ["a", "b", "c"]
+    shape, a = f.raw_i8("a")
+    assert shape == (3, 5, 7) and np.array_equal(a.reshape(shape), t["a"])
+    for k in ("b", "c"):
+        shape, v = f.raw_f32(k)
+        assert shape == t[k].shape and np.array_equal(v.reshape(shape), t[k])
+    with pytest.raises(convrot.CheckpointError, match="expected I8"):
+        f.raw_i8("b")
+    with pytest.raises(convrot.CheckpointError, match="missing tensor"):
+        f.raw_f32("d")
+
+
+def test_loader_refusals(tmp_path):
+    name = "blk.mlp.down"
+    assert convrot.ConvRotFile.open(str(tmp_path)) is None  # no file: None (convrot.rs:22-24)
+    path = str(tmp_path / convrot.FILE_NAME)
+    _write_layer(path, name, 4, 256)
+    f = convrot.ConvRotFile.open(str(tmp_path))
+    with pytest.raises(convrot.ConfigError):
+        f.linear(name, 256, 5, device="cpu")      # scale/zero length != output
+    with pytest.raises(convrot.ConfigError):
+        f.linear(name, 512, 4, device="cpu")      # qdata shape != [output, input]
+    with pytest.raises(convrot.ConfigError):
+        f.linear(name, 260, 4, device="cpu")      # input not a multiple of 256
+    with pytest.raises(convrot.CheckpointError):
+        f.linear("other", 256, 4, device="cpu")   # missing tensors
+    _write_layer(path, name, 4, 256, scale_dtype=np.float16)
+    with pytest.raises(convrot.CheckpointError, match="expected F32"):
+        convrot.ConvRotFile.open(str(tmp_path)).linear(name, 256, 4, device="cpu")
+
+
+def test_loader_rejects_a_corrupt_file(tmp_path):
+    path = tmp_path / "bad.safetensors"
+    path.write_bytes((10 ** 6).to_bytes(8, "little") + b"{}")
+    with pytest.raises(convrot.CheckpointError):
+        convrot.SafetensorsFile(str(path))
+    header = b'{"w": {"dtype": "I8", "shape": [4, 4], "data_offsets": [0, 64]}}'
+    path.write_bytes(len(header).to_bytes(8, "little") + header + bytes(16))
+    with pytest.raises(convrot.CheckpointError, match="outside"):
+        convrot.SafetensorsFile(str(path))
+    header = b'{"w": {"dtype": "I8", "shape": [4, 5], "data_offsets": [0, 16]}}'
+    path.write_bytes(len(header).to_bytes(8, "little") + header + bytes(16))
+    with pytest.raises(convrot.CheckpointError, match="payload"):
+        convrot.SafetensorsFile(str(path)).raw_i8("w")

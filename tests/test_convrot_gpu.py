@@ -170,3 +170,21 @@ def test_guards():
                              torch.ones(2, device="cuda"), torch.zeros(2, dtype=torch.int32, device="cuda"))
     with pytest.raises(RuntimeError):
         bad(torch.zeros((2, 256), device="cuda"))  # packed length disagrees: project() panics
+
+
+def test_layer_loaded_from_a_checkpoint(oracle, tmp_path):
+    # ConvRotFile::linear (convrot.rs:30-67) feeding the GPU layer, checked
+    # against the oracle route on the same tensors
+    from safetensors.numpy import save_file
+    rng = np.random.default_rng(21)
+    name, output, input = "transformer_blocks.3.ff.net.0.proj", 48, 768
+    q = rng.integers(-127, 128, (output, input), dtype=np.int8)
+    scale = rng.uniform(0.002, 0.02, output).astype(np.float32)
+    zero = rng.integers(-2, 3, output).astype(np.int8)
+    save_file({f"{name}._weight_qdata": q, f"{name}._weight_scale": scale,
+               f"{name}._weight_zero_point": zero}, str(tmp_path / convrot.FILE_NAME))
+    layer = convrot.ConvRotFile.open(str(tmp_path)).linear(name, input, output, precision=torch.float32)
+    x = rng.standard_normal((5, input)).astype(np.float32)
+    got = host(layer(dev(x)))
+    want = oracle.int8_gemm(oracle.rotate(x), q, scale, zero.astype(np.int32))
+    assert tolerance.rel_err(got, want.astype(np.float64)) <= tolerance.FP16_REL_TOL

@@ -125,6 +125,22 @@ def test_mfma_gemm_shapes(oracle, rows, width, columns):
     assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL
 
 
+@pytest.mark.parametrize("route", ["0", "2"])
+@pytest.mark.parametrize("rows,width,columns", [(5, 64, 33), (16, 4096, 4096), (13, 4112, 77),
+                                                (33, 1552, 200), (48, 16384, 17), (64, 8960, 1536),
+                                                (7, 16, 3)])
+def test_skinny_rows_on_both_routes(oracle, monkeypatch, route, rows, width, columns):
+    # 5..64 activation rows: the skinny MFMA kernel (route 0) and the tiled
+    # MFMA GEMM (OMNI_W8A16_ROUTE=2) against the f64 ground truth, with K
+    # tails that are not a multiple of 64 and ragged column counts.
+    monkeypatch.setenv("OMNI_W8A16_ROUTE", route)
+    rng = np.random.default_rng(rows * 3 + width + columns)
+    x, w, s, b = make(rng, rows, width, columns, bias=columns % 2 == 1)
+    got = host(oi.w8a16_linear(dev(x), dev(w), dev(s), None if b is None else dev(b)))
+    ref = gpu_f64_reference(x, w, s, b)
+    assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL, (route, rows, width, columns)
+
+
 def test_config5_small_vlm_layer(oracle):
     # BASELINE config 5, one layer: prefill M=1024 then a decode step M=1
     rng = np.random.default_rng(5)
