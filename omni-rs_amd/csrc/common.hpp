@@ -98,4 +98,44 @@ __device__ __forceinline__ float row_scale_of(float peak) {
     return row_scale;
 }
 
+// ---- LDS-DMA pipeline helpers shared by the MFMA GEMM kernels ----
+
+// Hardware workgroup id -> logical tile id, so that the workgroups one XCD
+// runs (hardware ids congruent mod 8) get a contiguous range of logical tiles.
+__device__ __forceinline__ int xcd_remap(int b, int total) {
+    constexpr int kXcds = 8;
+    const int per = total / kXcds, rem = total % kXcds;
+    const int xcd = b % kXcds, local = b / kXcds;
+    return xcd * per + (xcd < rem ? xcd : rem) + local;
+}
+
+
+#define OMNI_LDS __attribute__((address_space(3)))
+
+// One 16-byte-per-lane global -> LDS copy (global_load_lds_dwordx4). The
+// builtin needs a gfx950 target feature that the host compilation pass lacks,
+// so it is emitted in the device pass only.
+__device__ __forceinline__ void lds_copy16(const uint8_t* src, uint8_t* lds_dst) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_global_load_lds(src, (OMNI_LDS void*)lds_dst, 16, 0, 0);
+#endif
+}
+
+
+// s_waitcnt vmcnt(N) (and lgkmcnt(0) when LGKM0) for a compile-time N.
+template <int N, bool LGKM0 = false>
+__device__ __forceinline__ void s_waitcnt_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    // gfx9 encoding: vmcnt[3:0] | expcnt << 4 | lgkmcnt << 8 | vmcnt[5:4] << 14
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((LGKM0 ? 0 : 15) << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier for the LDS-DMA pipeline. __syncthreads() would wait for
+// every outstanding vector-memory operation (its release fence counts the
+// in-flight global->LDS copies as LDS writes); here the caller has already
+// waited for the copies that matter, and lgkmcnt(0) retires this wave's LDS
+// reads, so a plain s_barrier suffices. The memory clobber keeps the compiler
+// from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
 }  // namespace omni

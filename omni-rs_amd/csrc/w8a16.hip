@@ -481,6 +481,247 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a16_mfma_kernel(W
     }
 }
 
+// Persistent LDS-DMA ring GEMM on fp16 MFMA (K % 64 == 0), the W8A8 ring
+// kernel's pipeline with an f16 activation operand. One workgroup of 4 waves
+// (2 x 2) per CU walks BM x BN output tiles; each wave owns a BM/2 x BN/2
+// block of 32x32 f32 accumulators. A K tile is 64 elements: the stage holds
+// x's k 0..31 and k 32..63 as two [BM][64-byte] halves and W as one
+// [BN][64-byte] block, all copied by global_load_lds_dwordx4 with the W8A8
+// ring's XOR swizzle of 16-byte chunks, in a 3-stage ring.
+//
+// Fragments, per pair p of 16-k MFMA steps (k 32p .. 32p+31 of the tile):
+// lane (row r = lane % 32, h = lane / 32) reads W codes 32p + 16h .. +16 of
+// column r (one ds_read_b128, chunk 2p + h) and x halves 32p + 16h .. +16 of
+// row r (two ds_read_b128, chunks 2h and 2h + 1 of half p). The first
+// v_mfma_f32_32x32x16_f16 takes codes and halves 0..7, the second 8..15: A and
+// B share one lane-to-k map, so every product pairs matching k and the 32 k
+// of the pair are summed once. Codes become f16 exactly in registers (v_perm
+// and one subtract, as in the GEMV). The schedule is the W8A8 ring's: one
+// fragment read and one copy behind each MFMA, one barrier per K tile between
+// the two pairs, the next tile's first copies issued before the epilogue.
+template <int BM, int BN>
+__global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
+    constexpr int S = 3;
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int FM = WM / 32, FN = WN / 32;
+    constexpr int kRows = 2 * BM + BN;        // 64-byte stage rows: x k 0..31, x k 32..63, W
+    constexpr int kStage = kRows * 64;
+    constexpr int kCpw = kRows / 64;          // 1 KiB copies per wave per K tile
+    constexpr int kFrags = 2 * FM + FN;       // fragment reads per pair
+    static_assert(kRows % 64 == 0 && FM >= 1 && FN >= 1, "tile shape");
+    __shared__ __attribute__((aligned(1024))) uint8_t st0[kStage];
+    __shared__ __attribute__((aligned(1024))) uint8_t st1[kStage];
+    __shared__ __attribute__((aligned(1024))) uint8_t st2[kStage];
+    __shared__ float sScale[2][BN];
+    __shared__ float sBias[2][BN];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int tiles_m = (int)((a.rows + BM - 1) / BM);
+    const int tiles_n = (int)((a.columns + BN - 1) / BN);
+    const int total = tiles_m * tiles_n;
+    const int64_t K = a.width;
+    const int ktiles = (int)(K / 64);
+    const bool has_bias = a.bias != nullptr;
+    constexpr int kGroupM = 4;
+    auto stage = [&](int s) -> uint8_t* { return s == 0 ? st0 : s == 1 ? st1 : st2; };
+
+    // Copy c fills stage rows 16c .. 16c+15; lane l reads logical chunk
+    // (l % 4) ^ ((l / 16) % 4) of row l / 4, landing at physical chunk l % 4.
+    const int cp_row = lane >> 2;
+    const int cp_chunk = (lane & 3) ^ ((lane >> 4) & 3);
+    const uint8_t* src[kCpw];
+    int adv[kCpw];  // bytes per K tile: 128 for x rows (64 halves), 64 for W rows
+    int64_t m0 = 0, n0 = 0;
+    float p_sc = 0.0f, p_bi = 0.0f;
+    auto tile_origin = [&](int l, int64_t& tm0, int64_t& tn0) {
+        const int group_size = kGroupM * tiles_n;
+        const int first_m = (l / group_size) * kGroupM;
+        const int gm = min(tiles_m - first_m, kGroupM);
+        tm0 = (int64_t)__builtin_amdgcn_readfirstlane(first_m + (l % group_size) % gm) * BM;
+        tn0 = (int64_t)__builtin_amdgcn_readfirstlane((l % group_size) / gm) * BN;
+    };
+    auto setup_copies = [&]() {
+#pragma unroll
+        for (int j = 0; j < kCpw; ++j) {
+            const int c16 = (wave * kCpw + j) * 16;  // wave-uniform
+            if (c16 < 2 * BM) {
+                const int half = c16 >= BM;
+                const int64_t row = min(m0 + (c16 - half * BM) + cp_row, a.rows - 1);
+                src[j] = reinterpret_cast<const uint8_t*>(a.x + row * K) + half * 64 + cp_chunk * 16;
+                adv[j] = 128;
+            } else {
+                const int64_t row = min(n0 + (c16 - 2 * BM) + cp_row, a.columns - 1);
+                src[j] = reinterpret_cast<const uint8_t*>(a.w + row * K) + cp_chunk * 16;
+                adv[j] = 64;
+            }
+        }
+    };
+    auto load_params = [&](int64_t pn0) {
+        if (tid < BN) {
+            const int64_t col = min(pn0 + tid, a.columns - 1);
+            p_sc = (float)a.scale[col];
+            p_bi = has_bias ? (float)a.bias[col] : 0.0f;
+        }
+    };
+    auto store_params = [&](int par) {
+        if (tid < BN) {
+            sScale[par][tid] = p_sc;
+            sBias[par][tid] = p_bi;
+        }
+    };
+    auto copy_one = [&](int kt, int s, int j) {
+        const int64_t kk = min(kt, ktiles - 1);
+        lds_copy16(src[j] + kk * adv[j], stage(s) + wave * kCpw * 1024 + j * 1024);
+    };
+    auto copy_tile = [&](int kt, int s) {
+#pragma unroll
+        for (int j = 0; j < kCpw; ++j) copy_one(kt, s, j);
+    };
+
+    // Fragment offsets within a stage.
+    const int fr = lane & 31, fh = lane >> 5, fq = (fr >> 2) & 3;
+    auto offA = [&](int p, int j) { return (p * BM + wm * WM + fr) * 64 + (((2 * fh + j) ^ fq) << 4); };
+    auto offB = [&](int p) { return (2 * BM + wn * WN + fr) * 64 + (((2 * p + fh) ^ fq) << 4); };
+    v4i xa0[FM][2], xb0[FN], xa1[FM][2], xb1[FN];
+    // Fragment idx of a pair: A (i, j) for idx < 2 FM, else B idx - 2 FM.
+    auto read_frag = [&](int s, int p, int idx, v4i (&xa)[FM][2], v4i (&xb)[FN]) {
+        if (idx < 2 * FM)
+            xa[idx >> 1][idx & 1] =
+                *reinterpret_cast<const v4i*>(stage(s) + offA(p, idx & 1) + (idx >> 1) * 32 * 64);
+        else
+            xb[idx - 2 * FM] = *reinterpret_cast<const v4i*>(stage(s) + offB(p) + (idx - 2 * FM) * 32 * 64);
+    };
+    // One pair of MFMA steps on fragments xa/xb, with one read (and one copy)
+    // issued after each of the first MFMAs.
+    v16f acc[FM][FN];
+    auto pair_mfmas = [&](v4i (&xa)[FM][2], v4i (&xb)[FN], auto&& after) {
+#pragma unroll
+        for (int jn = 0; jn < FN; ++jn) {
+            const u32 wd[4] = {(u32)xb[jn][0], (u32)xb[jn][1], (u32)xb[jn][2], (u32)xb[jn][3]};
+            v2h h[8];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) i8x4_to_f16x4(wd[q], h[2 * q], h[2 * q + 1]);
+            const v8h b0 = {h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
+            const v8h b1 = {h[4][0], h[4][1], h[5][0], h[5][1], h[6][0], h[6][1], h[7][0], h[7][1]};
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                v8h a0, a1;
+                __builtin_memcpy(&a0, &xa[i][0], 16);
+                __builtin_memcpy(&a1, &xa[i][1], 16);
+                acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, acc[i][jn], 0, 0, 0);
+                after(2 * (jn * FM + i));
+                __builtin_amdgcn_sched_barrier(0);
+                acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b1, acc[i][jn], 0, 0, 0);
+                after(2 * (jn * FM + i) + 1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+
+    int L = xcd_remap(blockIdx.x, gridDim.x);
+    if (L >= total) return;
+    tile_origin(L, m0, n0);
+    setup_copies();
+    load_params(n0);
+    store_params(0);
+#pragma unroll
+    for (int u = 0; u < S - 1; ++u) copy_tile(u, u);
+    int parity = 0;
+
+    while (true) {
+        const int Ln = L + gridDim.x;
+        const bool more = Ln < total;
+        int64_t nm0 = 0, nn0 = 0;
+        if (more) {
+            tile_origin(Ln, nm0, nn0);
+            load_params(nn0);
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc[i][j] = v16f{};
+
+        s_waitcnt_vm<(S - 2) * kCpw, true>();
+        lds_barrier();
+#pragma unroll
+        for (int idx = 0; idx < kFrags; ++idx) read_frag(0, 0, idx, xa0, xb0);
+
+        for (int t0 = 0; t0 < ktiles; t0 += S) {
+#pragma unroll
+            for (int u = 0; u < S; ++u) {
+                const int kt = t0 + u;
+                if (kt < ktiles) {  // uniform across the workgroup
+                    // Pair 0 of tile kt; reads of pair 1.
+                    pair_mfmas(xa0, xb0, [&](int q) {
+                        if (q < kFrags) read_frag(u, 1, q, xa1, xb1);
+                    });
+                    s_waitcnt_vm<(S - 3) * kCpw, true>();
+                    lds_barrier();  // tile kt+1 landed everywhere; stage (u+S-1)%S is free
+                    // Pair 1 of tile kt; copies of tile kt+S-1; reads of tile kt+1, pair 0.
+                    pair_mfmas(xa1, xb1, [&](int q) {
+                        if (q < kCpw) copy_one(kt + S - 1, (u + S - 1) % S, q);
+                        if (q < kFrags) read_frag((u + 1) % S, 0, q, xa0, xb0);
+                    });
+                }
+            }
+        }
+
+        const int64_t em0 = m0, en0 = n0;
+        s_waitcnt_vm<(S - 2) * kCpw, true>();
+        lds_barrier();  // every wave is done reading the ring
+        if (more) {
+            m0 = nm0;
+            n0 = nn0;
+            setup_copies();
+            store_params(parity ^ 1);
+#pragma unroll
+            for (int u = 0; u < S - 1; ++u) copy_tile(u, u);
+        }
+
+        // Epilogue: out = f16(acc * scale[n] + bias[n]). 32x32 accumulator
+        // layout: lane holds column lane % 32, rows 8 (r / 4) + 4 (lane / 32) + r % 4.
+        const float* pScale = sScale[parity];
+        const float* pBias = sBias[parity];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int lc = wn * WN + j * 32 + fr;
+                const int64_t col = en0 + lc;
+                const float sc = pScale[lc];
+                const float bi = pBias[lc];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int64_t row = em0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * fh + (r & 3);
+                    if (row < a.rows && col < a.columns)
+                        __builtin_nontemporal_store((_Float16)(acc[i][j][r] * sc + bi),
+                                                    a.out + row * a.columns + col);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        if (!more) break;
+        L = Ln;
+        parity ^= 1;
+    }
+    s_waitcnt_vm<0>();  // copies of clamped K tiles may still be landing
+}
+
+template <int BM, int BN>
+hipError_t launch_ring16_cfg(const W8A16Args& a, hipStream_t stream) {
+    const int64_t tiles = ((a.rows + BM - 1) / BM) * ((a.columns + BN - 1) / BN);
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus = 256;
+    const int64_t grid = tiles < cus ? tiles : cus;
+    hipLaunchKernelGGL((w8a16_ring_kernel<BM, BN>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
 template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int GROUP_M>
 hipError_t launch_mfma16_cfg(const W8A16Args& a, hipStream_t stream) {
     auto kernel = w8a16_mfma_kernel<BM, BN, BK, WAVES_M, WAVES_N, GROUP_M>;
@@ -514,8 +755,33 @@ hipError_t launch_w8a16_skinny(const W8A16Args& a, hipStream_t stream) {
     return launch_skinny_cfg<4>(a, stream);
 }
 
+// OMNI_W8A16_TILE=<n> pins the prefill GEMM kernel (tuning and test aid):
+// 1 = tiled 128 x 128, 2 = tiled 64 x 64, 4/5 = ring 256 x 128 / 128 x 128
+// (K % 64 == 0 only). Read on every call.
+int w8a16_tile_override() {
+    const char* v = std::getenv("OMNI_W8A16_TILE");
+    return v ? std::atoi(v) : 0;
+}
+
 hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream) {
     if (a.rows == 0 || a.columns == 0) return hipSuccess;
+    const bool ring_ok = a.width % 64 == 0;
+    switch (w8a16_tile_override()) {
+        case 1: return launch_mfma16_cfg<128, 128, 64, 2, 2, 4>(a, stream);
+        case 2: return launch_mfma16_cfg<64, 64, 64, 2, 2, 4>(a, stream);
+        case 4: if (ring_ok) return launch_ring16_cfg<256, 128>(a, stream); break;
+        case 5: if (ring_ok) return launch_ring16_cfg<128, 128>(a, stream); break;
+        default: break;
+    }
+    // Measured on MI355X (config 5 and the BASELINE GEMM shapes): the ring
+    // kernel wins once K is long and its 256 x 128 tiles fill a round of CUs;
+    // the tiled kernels win on the small prefill shapes.
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus = 256;
+    const int64_t ring_tiles = ((a.rows + 255) / 256) * ((a.columns + 127) / 128);
+    if (ring_ok && a.width >= 3072 && ring_tiles >= cus) return launch_ring16_cfg<256, 128>(a, stream);
     const int64_t big_tiles = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
     if (big_tiles >= 512) return launch_mfma16_cfg<128, 128, 64, 2, 2, 4>(a, stream);
     return launch_mfma16_cfg<64, 64, 64, 2, 2, 4>(a, stream);

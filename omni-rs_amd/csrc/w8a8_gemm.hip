@@ -104,34 +104,6 @@ __global__ __launch_bounds__(256) void w8a8_scalar_kernel(W8A8Args a) {
 // MFMA lowering.
 // ---------------------------------------------------------------------------
 
-// Hardware workgroup id -> logical tile id, so that the workgroups one XCD
-// runs (hardware ids congruent mod 8) get a contiguous range of logical tiles.
-__device__ __forceinline__ int xcd_remap(int b, int total) {
-    constexpr int kXcds = 8;
-    const int per = total / kXcds, rem = total % kXcds;
-    const int xcd = b % kXcds, local = b / kXcds;
-    return xcd * per + (xcd < rem ? xcd : rem) + local;
-}
-
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int GROUP_M>
-struct MfmaCfgUnused {
-    static constexpr int kThreads = 64 * WAVES_M * WAVES_N;
-    static constexpr int WM = BM / WAVES_M;
-    static constexpr int WN = BN / WAVES_N;
-    static constexpr int FM = WM / 32;
-    static constexpr int FN = WN / 32;
-    static constexpr int kChunks = BK / 16;                 // 16-byte chunks per tile row
-    static constexpr int kALoads = (BM * kChunks + kThreads - 1) / kThreads;
-    static constexpr int kBLoads = (BN * kChunks + kThreads - 1) / kThreads;
-    static constexpr int kStageBytes = (BM + BN) * BK;
-    static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile is a multiple of 32x32");
-    static_assert(BK % 32 == 0 && kChunks <= 8, "K tile of 32..128 bytes");
-    // The last load slot of a thread may be idle when the tile's chunk count
-    // is not a multiple of the thread count.
-    static constexpr bool kAEven = (BM * kChunks) % kThreads == 0;
-    static constexpr bool kBEven = (BN * kChunks) % kThreads == 0;
-};
-
 // Physical 16-byte chunk slot of logical chunk c in tile row r. gfx950 LDS
 // has 64 four-byte banks and serves ds_read_b128 / ds_write_b128 16 lanes at
 // a time, i.e. one 256-byte window: 256 / (16 * kChunks) consecutive rows
@@ -406,17 +378,6 @@ __global__ __launch_bounds__(256, 1) void w8a8_mfma_kernel(W8A8Args a) {
 // (S divides the K-tile count) so every copy and read names its array
 // statically; the wait for K tile kt is vmcnt(copies issued after it),
 // leaving S-2 later tiles in flight, then one barrier per K tile.
-#define OMNI_LDS __attribute__((address_space(3)))
-
-// One 16-byte-per-lane global -> LDS copy (global_load_lds_dwordx4). The
-// builtin needs a gfx950 target feature that the host compilation pass lacks,
-// so it is emitted in the device pass only.
-__device__ __forceinline__ void lds_copy16(const uint8_t* src, uint8_t* lds_dst) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    __builtin_amdgcn_global_load_lds(src, (OMNI_LDS void*)lds_dst, 16, 0, 0);
-#endif
-}
-
 template <int BN, int WAVES_M>
 struct DmaCfg {
     static constexpr int BM = 128 * WAVES_M, BK = 64;
@@ -428,22 +389,6 @@ struct DmaCfg {
     static constexpr int kBCopies = BN / 64;
     static_assert(BM % (16 * kWaves) == 0, "A copies divide among waves");
 };
-
-// s_waitcnt vmcnt(N) (and lgkmcnt(0) when LGKM0) for a compile-time N.
-template <int N, bool LGKM0 = false>
-__device__ __forceinline__ void s_waitcnt_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    // gfx9 encoding: vmcnt[3:0] | expcnt << 4 | lgkmcnt << 8 | vmcnt[5:4] << 14
-    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((LGKM0 ? 0 : 15) << 8) | ((N >> 4) << 14));
-}
-
-// Workgroup barrier for the LDS-DMA pipeline. __syncthreads() would wait for
-// every outstanding vector-memory operation (its release fence counts the
-// in-flight global->LDS copies as LDS writes); here the caller has already
-// waited for the copies that matter, and lgkmcnt(0) retires this wave's LDS
-// reads, so a plain s_barrier suffices. The memory clobber keeps the compiler
-// from moving LDS accesses across it.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 template <int BN, int WAVES_M, int S, bool OUT16, bool DUMP>
 __global__ __launch_bounds__(128 * WAVES_M, 512 / (128 * WAVES_M)) void w8a8_dma_kernel(W8A8Args a) {
@@ -634,9 +579,10 @@ __global__ __launch_bounds__(128 * WAVES_M, 512 / (128 * WAVES_M)) void w8a8_dma
 // most of an MFMA group to land, no copy burst holds up an MFMA, and the only
 // barrier sits between two MFMA groups. (With one wave per SIMD a copy that
 // waits for the CU's texture unit blocks its wave's next MFMA: measured on
-// MI355X, copies issued in a burst and MFMAs do not overlap at all.) The next output tile's first copies are issued
-// before this tile's epilogue, whose per-row and per-column values sit in a
-// parity-double-buffered LDS block. Epilogue stores of partial tiles are
+// MI355X, copies issued in a burst and MFMAs do not overlap at all.) The
+// next output tile's first copies are issued before this tile's epilogue,
+// whose per-row and per-column values sit in a parity-double-buffered LDS
+// block. Epilogue stores of partial tiles are
 // unconditional too: rows and columns past the matrix were loaded clamped to
 // the last row and column, so their values equal the last row's (column's)
 // and are stored there, a duplicate write of the same value.

@@ -141,6 +141,21 @@ def test_skinny_rows_on_both_routes(oracle, monkeypatch, route, rows, width, col
     assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL, (route, rows, width, columns)
 
 
+@pytest.mark.parametrize("tile", ["1", "2", "4", "5"])
+@pytest.mark.parametrize("rows,width,columns", [(300, 512, 200), (1024, 1536, 1536), (257, 8960, 129),
+                                                (197, 4096, 640), (65, 64, 33)])
+def test_every_prefill_kernel(oracle, monkeypatch, tile, rows, width, columns):
+    # OMNI_W8A16_TILE pins one prefill kernel: the tiled GEMMs (1, 2) and the
+    # LDS-DMA ring GEMMs (4 = 256 x 128, 5 = 128 x 128); ragged rows/columns,
+    # bias, against the f64 ground truth
+    monkeypatch.setenv("OMNI_W8A16_TILE", tile)
+    rng = np.random.default_rng(rows + width + columns + int(tile))
+    x, w, s, b = make(rng, rows, width, columns, bias=True)
+    got = host(oi.w8a16_linear(dev(x), dev(w), dev(s), dev(b)))
+    ref = gpu_f64_reference(x, w, s, b)
+    assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL, (tile, rows, width, columns)
+
+
 def test_config5_small_vlm_layer(oracle):
     # BASELINE config 5, one layer: prefill M=1024 then a decode step M=1
     rng = np.random.default_rng(5)
