@@ -163,6 +163,22 @@ int omni_w8a16_gemm(const uint16_t* x, const int8_t* w, const uint16_t* scale,
                     const uint16_t* bias, int64_t rows, int64_t columns, int64_t width,
                     uint16_t* out, void* stream);
 
+/* Weight-only int4 linear (W4A16), the MiniCPM-V pack-quantized format.
+ * Replaces the packed-int4 matmul of crates/minicpm-v/src/quant.rs:43-58
+ * (PackedWeight::matmul_transpose, x @ W^T) with the weight layout that
+ * load_packed reads (:145-201): w_packed [columns][width / 2] bytes, two
+ * values per byte, low nibble first, each stored plus 8 (unpack_int4,
+ * :22-29); scale_bf16 [columns][width / group] bf16, one per group of
+ * consecutive values along the row (:74-81, :186-200, GROUP_SIZE = 128).
+ *   out[m][n] = f16(sum_k x[m][k] * (q[n][k] * scale[n][k / group]) + bias[n])
+ * x f16 [rows][width], bias f16 [columns] or NULL, out f16 [rows][columns].
+ * width % group == 0 and group % 32 == 0, else OMNI_NOT_HANDLED; x and
+ * w_packed 16-byte aligned. rows <= 4 (width <= 32768) runs the HBM-bound
+ * GEMV, rows <= 64 the skinny MFMA kernel, more rows the fp16-MFMA GEMM. */
+int omni_w4a16_gemm(const uint16_t* x, const uint8_t* w_packed, const uint16_t* scale_bf16,
+                    int64_t group, const uint16_t* bias, int64_t rows, int64_t columns,
+                    int64_t width, uint16_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -318,4 +318,39 @@ int omni_w8a16_gemm(const uint16_t* x, const int8_t* w, const uint16_t* scale,
     return hip_status(omni::launch_w8a16_mfma(a, s), "w8a16 mfma launch");
 }
 
+int omni_w4a16_gemm(const uint16_t* x, const uint8_t* w_packed, const uint16_t* scale_bf16,
+                    int64_t group, const uint16_t* bias, int64_t rows, int64_t columns,
+                    int64_t width, uint16_t* out, void* stream) {
+    if (rows < 0 || columns < 0 || width < 0 || group <= 0)
+        return fail(OMNI_BAD_ARGUMENT, "w4a16_gemm: bad sizes");
+    // 32 values (16 bytes) per GEMV lane, and a lane's values in one group.
+    if (width % 32 != 0 || group % 32 != 0 || width % group != 0)
+        return fail(OMNI_NOT_HANDLED, "w4a16_gemm: width %lld / group %lld (need width %% group == 0, group %% 32 == 0)",
+                    (long long)width, (long long)group);
+    if (rows == 0 || columns == 0) return OMNI_OK;
+    if (!x || !w_packed || !scale_bf16 || !out) return fail(OMNI_BAD_ARGUMENT, "w4a16_gemm: null pointer");
+    if (!aligned(x, 16) || !aligned(w_packed, 16))
+        return fail(OMNI_BAD_ARGUMENT, "w4a16_gemm: x and w_packed must be 16-byte aligned");
+    if (((rows + 63) / 64) * ((columns + 63) / 64) > 0x7fffffffLL)
+        return fail(OMNI_BAD_ARGUMENT, "w4a16_gemm: problem too large");
+    int st = check_current_device();
+    if (st != OMNI_OK) return st;
+    omni::W8A16Args a;
+    a.x = reinterpret_cast<const _Float16*>(x);
+    a.w = reinterpret_cast<const int8_t*>(w_packed);
+    a.scale = nullptr;
+    a.bias = reinterpret_cast<const _Float16*>(bias);
+    a.out = reinterpret_cast<_Float16*>(out);
+    a.rows = rows;
+    a.columns = columns;
+    a.width = width;
+    a.gscale = scale_bf16;
+    a.group = group;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (rows <= 4 && width <= 32768)
+        return hip_status(omni::launch_w4a16_gemv(a, s), "w4a16 gemv launch");
+    if (rows <= 64) return hip_status(omni::launch_w4a16_skinny(a, s), "w4a16 skinny launch");
+    return hip_status(omni::launch_w4a16_mfma(a, s), "w4a16 mfma launch");
+}
+
 }  // extern "C"

@@ -35,15 +35,23 @@ hipError_t launch_w8a8_scalar(const W8A8Args& a, hipStream_t stream);
 
 struct W8A16Args {
     const _Float16* x;      // [rows][width]
-    const int8_t* w;        // [columns][width]
-    const _Float16* scale;  // [columns]
+    const int8_t* w;        // [columns][width] int8, or [columns][width / 2] packed int4
+    const _Float16* scale;  // [columns] (int8 weights)
     const _Float16* bias;   // [columns] or null
     _Float16* out;          // [rows][columns]
     int64_t rows, columns, width;
+    const uint16_t* gscale = nullptr;  // int4 weights: bf16 [columns][width / group]
+    int64_t group = 0;                  // int4 weights: values per scale along K
 };
 
 hipError_t launch_w8a16_gemv(const W8A16Args& a, hipStream_t stream);
 hipError_t launch_w8a16_skinny(const W8A16Args& a, hipStream_t stream);
 hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream);
+
+// W4A16 (w8a16.hip): packed int4 weights (two per byte, low nibble first,
+// offset by 8) with bf16 scales per group of K values.
+hipError_t launch_w4a16_gemv(const W8A16Args& a, hipStream_t stream);
+hipError_t launch_w4a16_skinny(const W8A16Args& a, hipStream_t stream);
+hipError_t launch_w4a16_mfma(const W8A16Args& a, hipStream_t stream);
 
 }  // namespace omni

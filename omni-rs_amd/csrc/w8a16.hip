@@ -50,6 +50,40 @@ __device__ __forceinline__ void i8x4_to_f16x4(u32 word, v2h& lo, v2h& hi) {
     hi = bits_half2(p1) - k1152;
 }
 
+// Eight int4 codes of `word` (low nibble first, each stored plus 8, as
+// crates/minicpm-v/src/quant.rs:22-29 unpacks them) -> four f16 pairs in k
+// order (n0,n1) (n2,n3) (n4,n5) (n6,n7), exact: bytes [n, 0x64] are the f16
+// 1024 + n, and one packed subtract of 1032 leaves n - 8.
+__device__ __forceinline__ void i4x8_to_f16x8(u32 word, v2h (&h)[4]) {
+    const u32 lo = word & 0x0F0F0F0Fu;         // n0 n2 n4 n6
+    const u32 hi = (word >> 4) & 0x0F0F0F0Fu;  // n1 n3 n5 n7
+    const v2h k1032 = {(_Float16)1032.0f, (_Float16)1032.0f};
+    h[0] = bits_half2(__builtin_amdgcn_perm(hi, lo, 0x0C040C00u) | 0x64006400u) - k1032;
+    h[1] = bits_half2(__builtin_amdgcn_perm(hi, lo, 0x0C050C01u) | 0x64006400u) - k1032;
+    h[2] = bits_half2(__builtin_amdgcn_perm(hi, lo, 0x0C060C02u) | 0x64006400u) - k1032;
+    h[3] = bits_half2(__builtin_amdgcn_perm(hi, lo, 0x0C070C03u) | 0x64006400u) - k1032;
+}
+
+// A bf16 scale (quant.rs:74-81) as f32 (exact) and as f16 (exact for scales
+// in f16's normal range, 2^-14 .. 65504).
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((u32)b << 16); }
+
+// 16 int4 codes (two words) times one scale -> 16 halves in k order:
+// f16(q * s), the dequantised value the reference's F16 route rounds to
+// (quant.rs:186-200): q * s is exact in f32 and the packed f16 multiply
+// rounds it once, like the f32 -> f16 cast.
+__device__ __forceinline__ void i4x16_dequant(u32 w0, u32 w1, _Float16 s, v2h (&h)[8]) {
+    v2h a[4], b[4];
+    i4x8_to_f16x8(w0, a);
+    i4x8_to_f16x8(w1, b);
+    const v2h s2 = {s, s};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        h[i] = a[i] * s2;
+        h[4 + i] = b[i] * s2;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Decode GEMV.
 // ---------------------------------------------------------------------------
@@ -336,6 +370,174 @@ hipError_t launch_skinny_cfg(const W8A16Args& a, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------
+// W4A16: packed int4 weights, bf16 scales per group of K values.
+// ---------------------------------------------------------------------------
+
+// Decode GEMV (rows <= 4) for int4 weights: the W8A16 GEMV's design with 32
+// codes (16 bytes) per lane per row: a lane's 32-value chunk lies in one
+// scale group (group % 32 == 0), so the chunk's dot is taken on the exact
+// codes and multiplied by its scale once. A workgroup of T = 64 * ceil(K /
+// 2048) lanes owns R weight rows; every weight load is issued up front.
+template <int MR, int R>
+__global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W8A16Args a) {
+    constexpr int V = R * MR;
+    static_assert((V & (V - 1)) == 0 && V <= 64, "power-of-two partial count");
+    __shared__ float s_part[16][V];
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int T = blockDim.x;
+    const int64_t K = a.width;
+    const int64_t chunks = K / 32;
+    const int64_t gpr = K / a.group;  // scale groups per weight row
+    const int64_t n0 = (int64_t)blockIdx.x * R;
+    const bool live = tid < chunks;
+    const int64_t c = live ? tid : chunks - 1;  // clamped: meets zero activations
+
+    // x: 32 halves of each row's chunk as 16 f16 pairs.
+    v2h xr[MR][16];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        if (live && m < a.rows) {
+            const uint4* p = reinterpret_cast<const uint4*>(a.x + m * K + c * 32);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint4 v = p[q];
+                xr[m][4 * q] = bits_half2(v.x);
+                xr[m][4 * q + 1] = bits_half2(v.y);
+                xr[m][4 * q + 2] = bits_half2(v.z);
+                xr[m][4 * q + 3] = bits_half2(v.w);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) xr[m][e] = v2h{};
+        }
+    }
+    v4u wv[R];
+    float sc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t n = n0 + r < a.columns ? n0 + r : a.columns - 1;
+        wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(a.w + n * (K / 2) + c * 16));
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t n = n0 + r < a.columns ? n0 + r : a.columns - 1;
+        sc[r] = bf16_to_f32(a.gscale[n * gpr + (c * 32) / a.group]);
+    }
+    const int64_t n_ep = min(n0 + (tid / MR) % R, a.columns - 1);
+    const _Float16 bi_h = a.bias ? a.bias[n_ep] : (_Float16)0.0f;
+
+    float part[V];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float d[MR];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) d[m] = 0.0f;
+        const u32 words[4] = {wv[r].x, wv[r].y, wv[r].z, wv[r].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            v2h h[4];
+            i4x8_to_f16x8(words[q], h);
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) d[m] = __builtin_amdgcn_fdot2(h[j], xr[m][4 * q + j], d[m], false);
+        }
+#pragma unroll
+        for (int m = 0; m < MR; ++m) part[r * MR + m] = d[m] * sc[r];
+    }
+    Fold<V, 32>::run(part, lane);
+    if ((lane & (64 / V - 1)) == 0) s_part[wave][fold_index<V>(lane)] = part[0];
+    __syncthreads();
+    if (tid < V) {
+        const int r = tid / MR, m = tid % MR;
+        const int64_t n = n0 + r;
+        if (n < a.columns && m < a.rows) {
+            float acc = 0.0f;
+            for (int w = 0; w < T / 64; ++w) acc += s_part[w][tid];
+            a.out[(int64_t)m * a.columns + n] = (_Float16)(acc + (float)bi_h);
+        }
+    }
+}
+
+// Skinny GEMM (5..64 rows) for int4 weights: the W8A16 skinny kernel with
+// 16 codes (8 bytes) per lane per 64-value K step, dequantised to f16(q * s).
+template <int MB>
+__global__ __launch_bounds__(1024) void w4a16_skinny_kernel(W8A16Args a) {
+    __shared__ float s_part[16][MB][256];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t K = a.width;
+    const int64_t gpr = K / a.group;
+    const int64_t n0 = (int64_t)blockIdx.x * 16;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int64_t wn = n0 + r16 < a.columns ? n0 + r16 : a.columns - 1;  // clamped: never stored
+    const uint8_t* wrow = reinterpret_cast<const uint8_t*>(a.w) + wn * (K / 2);
+    const uint16_t* srow = a.gscale + wn * gpr;
+    const _Float16* xrow[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+        const int64_t m = mb * 16 + r16 < a.rows ? mb * 16 + r16 : a.rows - 1;
+        xrow[mb] = a.x + m * K;
+    }
+    v4f_t acc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
+    const int64_t steps = (K + 63) / 64;
+    auto step = [&](int64_t st) {
+        const int64_t k = st * 64 + 16 * g;
+        uint2 wv = make_uint2(0x88888888u, 0x88888888u);  // codes 0
+        _Float16 s = (_Float16)0.0f;
+        uint4 xv[MB][2];
+        if (k < K) {  // K % 16 == 0: a lane's 16 values are wholly inside or outside
+            wv = *reinterpret_cast<const uint2*>(wrow + k / 2);
+            s = (_Float16)bf16_to_f32(srow[k / a.group]);
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                xv[mb][0] = reinterpret_cast<const uint4*>(xrow[mb] + k)[0];
+                xv[mb][1] = reinterpret_cast<const uint4*>(xrow[mb] + k)[1];
+            }
+        } else {
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) xv[mb][0] = xv[mb][1] = make_uint4(0, 0, 0, 0);
+        }
+        v2h h[8];
+        i4x16_dequant(wv.x, wv.y, s, h);
+        const v8h b0 = {h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
+        const v8h b1 = {h[4][0], h[4][1], h[5][0], h[5][1], h[6][0], h[6][1], h[7][0], h[7][1]};
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+            v8h a0, a1;
+            __builtin_memcpy(&a0, &xv[mb][0], 16);
+            __builtin_memcpy(&a1, &xv[mb][1], 16);
+            acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b0, acc[mb], 0, 0, 0);
+            acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b1, acc[mb], 0, 0, 0);
+        }
+    };
+    int64_t st = wave;
+    for (; st + 16 < steps; st += 32) {
+        step(st);
+        step(st + 16);
+    }
+    if (st < steps) step(st);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s_part[wave][mb][(4 * g + r) * 16 + r16] = acc[mb][r];
+    __syncthreads();
+    if (tid < MB * 256) {
+        const int mb = tid >> 8, e = tid & 255;
+        const int64_t m = mb * 16 + (e >> 4), n = n0 + (e & 15);
+        if (m < a.rows && n < a.columns) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 16; ++w) sum += s_part[w][mb][e];
+            const float bi = a.bias ? (float)a.bias[n] : 0.0f;
+            a.out[m * a.columns + n] = (_Float16)(sum + bi);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Prefill GEMM on fp16 MFMA.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int xcd_remap16(int b, int total) {
@@ -346,7 +548,9 @@ __device__ __forceinline__ int xcd_remap16(int b, int total) {
 }
 
 // Tile rows hold BK f16 = 2*BK bytes; 16-byte chunks swizzled by row.
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int GROUP_M>
+// WBITS 8: int8 weights, per-column f16 scale in the epilogue; WBITS 4:
+// packed int4 weights dequantised to f16(q * s) per K group while staged.
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int GROUP_M, int WBITS = 8>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a16_mfma_kernel(W8A16Args a) {
     constexpr int kThreads = 64 * WAVES_M * WAVES_N;
     constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
@@ -396,8 +600,18 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a16_mfma_kernel(W
             const int id = tid + i * kThreads;
             const int r = id / (BK / 16), c = id % (BK / 16);
             const int64_t gr = n0 + r, gk = k0 + c * 16;
-            rb[i] = (gr < a.columns && gk < K) ? *reinterpret_cast<const uint4*>(a.w + gr * K + gk)
-                                               : make_uint4(0, 0, 0, 0);
+            if constexpr (WBITS == 8) {
+                rb[i] = (gr < a.columns && gk < K) ? *reinterpret_cast<const uint4*>(a.w + gr * K + gk)
+                                                   : make_uint4(0, 0, 0, 0);
+            } else {
+                // 16 codes = 8 bytes, and their group's bf16 scale in .z
+                if (gr < a.columns && gk < K) {
+                    const uint2 q = *reinterpret_cast<const uint2*>(a.w + gr * (K / 2) + gk / 2);
+                    rb[i] = make_uint4(q.x, q.y, a.gscale[gr * (K / a.group) + gk / a.group], 0);
+                } else {
+                    rb[i] = make_uint4(0x88888888u, 0x88888888u, 0, 0);  // codes 0
+                }
+            }
         }
     };
     auto store_tile = [&](int buf) {
@@ -414,10 +628,14 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a16_mfma_kernel(W
             const int id = tid + i * kThreads;
             const int r = id / (BK / 16), c = id % (BK / 16);
             // 16 codes -> 16 halves = two 16-byte chunks 2c and 2c+1.
-            const u32 words[4] = {rb[i].x, rb[i].y, rb[i].z, rb[i].w};
             v2h h[8];
+            if constexpr (WBITS == 8) {
+                const u32 words[4] = {rb[i].x, rb[i].y, rb[i].z, rb[i].w};
 #pragma unroll
-            for (int q = 0; q < 4; ++q) i8x4_to_f16x4(words[q], h[2 * q], h[2 * q + 1]);
+                for (int q = 0; q < 4; ++q) i8x4_to_f16x4(words[q], h[2 * q], h[2 * q + 1]);
+            } else {
+                i4x16_dequant(rb[i].x, rb[i].y, (_Float16)bf16_to_f32((uint16_t)rb[i].z), h);
+            }
             uint4 lo = make_uint4(half2_bits(h[0]), half2_bits(h[1]), half2_bits(h[2]), half2_bits(h[3]));
             uint4 hi = make_uint4(half2_bits(h[4]), half2_bits(h[5]), half2_bits(h[6]), half2_bits(h[7]));
             *reinterpret_cast<uint4*>(dB + r * kRowBytes + swz(r, 2 * c) * 16) = lo;
@@ -468,7 +686,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a16_mfma_kernel(W
     for (int j = 0; j < FN; ++j) {
         const int64_t col = n0 + wn * WN + j * 32 + (lane & 31);
         if (col >= a.columns) continue;
-        const float sc = (float)a.scale[col];
+        const float sc = WBITS == 8 ? (float)a.scale[col] : 1.0f;  // int4: scaled per group already
         const float bias = a.bias ? (float)a.bias[col] : 0.0f;
 #pragma unroll
         for (int i = 0; i < FM; ++i)
@@ -722,9 +940,9 @@ hipError_t launch_ring16_cfg(const W8A16Args& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int GROUP_M>
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int GROUP_M, int WBITS = 8>
 hipError_t launch_mfma16_cfg(const W8A16Args& a, hipStream_t stream) {
-    auto kernel = w8a16_mfma_kernel<BM, BN, BK, WAVES_M, WAVES_N, GROUP_M>;
+    auto kernel = w8a16_mfma_kernel<BM, BN, BK, WAVES_M, WAVES_N, GROUP_M, WBITS>;
     const size_t smem = 2 * (size_t)(BM + BN) * BK * 2;
     if (smem > 65536) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
@@ -785,6 +1003,38 @@ hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream) {
     const int64_t big_tiles = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
     if (big_tiles >= 512) return launch_mfma16_cfg<128, 128, 64, 2, 2, 4>(a, stream);
     return launch_mfma16_cfg<64, 64, 64, 2, 2, 4>(a, stream);
+}
+
+hipError_t launch_w4a16_gemv(const W8A16Args& a, hipStream_t stream) {
+    if (a.rows == 0 || a.columns == 0) return hipSuccess;
+    const int64_t chunks = a.width / 32;
+    const int64_t T = ((chunks + 63) / 64) * 64;
+    if (T > 1024) return hipErrorInvalidValue;  // the caller keeps width <= 32768
+    constexpr int R = 4;
+    const dim3 grid((unsigned)((a.columns + R - 1) / R)), block((unsigned)T);
+    switch (a.rows) {
+        case 1: hipLaunchKernelGGL((w4a16_gemv_kernel<1, R>), grid, block, 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((w4a16_gemv_kernel<2, R>), grid, block, 0, stream, a); break;
+        default: hipLaunchKernelGGL((w4a16_gemv_kernel<4, R>), grid, block, 0, stream, a); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_w4a16_skinny(const W8A16Args& a, hipStream_t stream) {
+    if (a.rows == 0 || a.columns == 0) return hipSuccess;
+    const dim3 grid((unsigned)((a.columns + 15) / 16)), block(1024);
+    if (a.rows <= 16) hipLaunchKernelGGL((w4a16_skinny_kernel<1>), grid, block, 0, stream, a);
+    else if (a.rows <= 32) hipLaunchKernelGGL((w4a16_skinny_kernel<2>), grid, block, 0, stream, a);
+    else if (a.rows <= 48) hipLaunchKernelGGL((w4a16_skinny_kernel<3>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((w4a16_skinny_kernel<4>), grid, block, 0, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_w4a16_mfma(const W8A16Args& a, hipStream_t stream) {
+    if (a.rows == 0 || a.columns == 0) return hipSuccess;
+    const int64_t big_tiles = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
+    if (big_tiles >= 512) return launch_mfma16_cfg<128, 128, 64, 2, 2, 4, 4>(a, stream);
+    return launch_mfma16_cfg<64, 64, 64, 2, 2, 4, 4>(a, stream);
 }
 
 }  // namespace omni

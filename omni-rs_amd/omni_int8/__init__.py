@@ -20,7 +20,7 @@ from ._lib import (OMNI_F16, OMNI_F32, OMNI_LOWERING_AUTO, OMNI_LOWERING_MFMA,
                    OMNI_LOWERING_SCALAR, OMNI_NOT_HANDLED, OMNI_OK, OmniError)
 
 __all__ = [
-    "try_int8_gemm", "quantize_rows", "w8a8_gemm", "w8a16_linear", "pack_i8",
+    "try_int8_gemm", "quantize_rows", "w8a8_gemm", "w8a16_linear", "w4a16_linear", "pack_i8",
     "arch_supported", "lowering", "OmniError",
     "OMNI_LOWERING_AUTO", "OMNI_LOWERING_MFMA", "OMNI_LOWERING_SCALAR",
 ]
@@ -189,6 +189,36 @@ def w8a16_linear(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor,
     st = _lib.check(_lib.lib().omni_w8a16_gemm(
         _ptr(x2), _ptr(w), _ptr(scale.contiguous()), _ptr(None if bias is None else bias.contiguous()),
         x2.shape[0], columns, width, _ptr(out), _stream(device)))
+    if st == OMNI_NOT_HANDLED:
+        raise ValueError(_lib.last_error())
+    return out.reshape(*lead, columns)
+
+
+def w4a16_linear(x: torch.Tensor, w_packed: torch.Tensor, scale: torch.Tensor,
+                 bias: Optional[torch.Tensor] = None, group: int = 128) -> torch.Tensor:
+    """Weight-only int4 linear in the MiniCPM-V pack-quantized format
+    (crates/minicpm-v/src/quant.rs:22-201): ``x @ W^T`` with
+    ``W[n][k] = q[n][k] * scale[n][k // group]``.
+
+    x f16 [..., width]; w_packed uint8 [columns, width // 2] (two values per
+    byte, low nibble first, stored plus 8); scale bf16 [columns, width // group];
+    bias f16 [columns] -> f16 [..., columns]."""
+    lead = x.shape[:-1]
+    width = x.shape[-1]
+    x2 = x.reshape(-1, width)
+    device = _require_gpu(x2, w_packed, scale, bias)
+    if x2.dtype != torch.float16 or w_packed.dtype != torch.uint8 or scale.dtype != torch.bfloat16:
+        raise ValueError("w4a16_linear wants f16 x, uint8 packed weights, bf16 scales")
+    columns = w_packed.shape[0]
+    if (w_packed.shape[-1] * 2 != width or scale.numel() != columns * (width // group)
+            or (bias is not None and (bias.dtype != torch.float16 or bias.numel() != columns))):
+        raise ValueError("w4a16_linear: shapes disagree")
+    x2 = x2.contiguous()
+    out = torch.empty((x2.shape[0], columns), dtype=torch.float16, device=device)
+    st = _lib.check(_lib.lib().omni_w4a16_gemm(
+        _ptr(x2), _ptr(w_packed.contiguous()), _ptr(scale.contiguous()), group,
+        _ptr(None if bias is None else bias.contiguous()), x2.shape[0], columns, width, _ptr(out),
+        _stream(device)))
     if st == OMNI_NOT_HANDLED:
         raise ValueError(_lib.last_error())
     return out.reshape(*lead, columns)

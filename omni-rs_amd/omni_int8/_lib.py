@@ -39,6 +39,7 @@ SIGNATURES = {
     "omni_try_int8_gemm": (_INT, [_P, _INT, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _P,
                                   ctypes.c_size_t, _P]),
     "omni_w8a16_gemm": (_INT, [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P]),
+    "omni_w4a16_gemm": (_INT, [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _P]),
     "omni_convrot_quantize_rows": (_INT, [_P, _INT, _I64, _I64, _I64, _I64, _P, _P, _P, _P]),
     "omni_convrot_linear": (_INT, [_P, _INT, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _INT,
                                    _P, ctypes.c_size_t, _P]),

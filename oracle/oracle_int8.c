@@ -388,3 +388,80 @@ void oracle_rotate(const float* x, int64_t rows, int64_t width, int64_t group, f
         }
     free(h);
 }
+
+/* ---- W4A16 (crates/minicpm-v/src/quant.rs) --------------------------------- */
+
+/* quant.rs:22-29 (unpack_int4): two values per byte, low nibble first, each
+ * stored as an unsigned nibble offset by 8 (8 means 0, 0 means -8). */
+void oracle_unpack_int4(const uint8_t* packed, int64_t bytes, int8_t* out)
+{
+    for (int64_t i = 0; i < bytes; ++i) {
+        out[2 * i] = (int8_t)((int)(packed[i] & 0xF) - 8);
+        out[2 * i + 1] = (int8_t)((int)(packed[i] >> 4) - 8);
+    }
+}
+
+/* quant.rs:74-81 (bf16_scale_bytes): a bf16 is the top half of an f32. */
+float oracle_bf16_to_f32(uint16_t b)
+{
+    uint32_t u = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* quant.rs:186-200 (load_packed, Dequantize mode): each run of `group`
+ * consecutive values of the row-major [rows][width] weight times the next
+ * scale, in f32; then, for the F16 precision, rounded once to f16. */
+void oracle_w4a16_dequant(const uint8_t* packed, const uint16_t* scale_bf16, int64_t rows,
+                          int64_t width, int64_t group, int f16_round, float* w_deq)
+{
+    const int64_t n = rows * width;
+    int8_t* v = (int8_t*)malloc((size_t)n);
+    oracle_unpack_int4(packed, n / 2, v);
+    for (int64_t i = 0; i < n; ++i) {
+        float d = (float)v[i] * oracle_bf16_to_f32(scale_bf16[i / group]);
+        w_deq[i] = f16_round ? oracle_f16_to_f32(oracle_f32_to_f16(d)) : d;
+    }
+    free(v);
+}
+
+/* Ground truth: x @ (q * s)^T (+ bias) in f64 (every product is exact). */
+void oracle_w4a16_f64(const uint16_t* x, int64_t rows, int64_t width, const uint8_t* packed,
+                      const uint16_t* scale_bf16, int64_t group, const uint16_t* bias,
+                      int64_t columns, double* out)
+{
+    float* w = (float*)malloc((size_t)(columns * width) * sizeof(float));
+    oracle_w4a16_dequant(packed, scale_bf16, columns, width, group, 0, w);
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < columns; ++c) {
+            double s = 0.0;
+            for (int64_t k = 0; k < width; ++k)
+                s += (double)oracle_f16_to_f32(x[r * width + k]) * (double)w[c * width + k];
+            if (bias)
+                s += (double)oracle_f16_to_f32(bias[c]);
+            out[r * columns + c] = s;
+        }
+    free(w);
+}
+
+/* The reference's CPU route in F16 precision: dequantise at load to f16
+ * (quant.rs:186-200), then x @ w^T (quant.rs:53-58) with f32 accumulation in
+ * k order, output rounded to f16. */
+void oracle_w4a16_gemm(const uint16_t* x, int64_t rows, int64_t width, const uint8_t* packed,
+                       const uint16_t* scale_bf16, int64_t group, const uint16_t* bias,
+                       int64_t columns, uint16_t* out)
+{
+    float* w = (float*)malloc((size_t)(columns * width) * sizeof(float));
+    oracle_w4a16_dequant(packed, scale_bf16, columns, width, group, 1, w);
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < columns; ++c) {
+            float acc = 0.0f;
+            for (int64_t k = 0; k < width; ++k)
+                acc += oracle_f16_to_f32(x[r * width + k]) * w[c * width + k];
+            if (bias)
+                acc += oracle_f16_to_f32(bias[c]);
+            out[r * columns + c] = oracle_f32_to_f16(acc);
+        }
+    free(w);
+}

@@ -34,6 +34,14 @@
  *   oracle_w8a16_f64 — numpy float64 matmul of the same operands.
  *   oracle_w8a16_gemm — within 1e-2 relative of oracle_w8a16_f64 (the
  *       tolerance the path is specified to) and exact on integer-valued cases.
+ *   oracle_unpack_int4 — every byte value against the rule of quant.rs:22-29
+ *       and its own test values (8 -> 0, 0 -> -8, 0xF -> 7).
+ *   oracle_bf16_to_f32 — every bf16 bit pattern against numpy's float32 top
+ *       half (the definition of bf16).
+ *   oracle_w4a16_dequant / _f64 / _gemm — the synthetic weights of
+ *       quant.rs:419-462 round-trip through pack/unpack exactly; the route is
+ *       within the reference test's 5e-2 (quant.rs:503) of the f64 truth and
+ *       equals numpy restating dequantise -> f16 -> f32 dot on small cases.
  *   oracle_hadamard / oracle_rotate — symmetry, H*H = I within 1e-4 and the
  *       float-matmul cancellation (convrot.rs:169-220); the 4x4 base
  *       H4[a][b] = -1 iff a^b == 3 (convrot.rs:139-140); scipy.linalg.hadamard
@@ -77,6 +85,17 @@ void oracle_w8a16_gemm(const uint16_t* x, int64_t rows, int64_t width, const int
 int oracle_hadamard_sign_negative(uint64_t row, uint64_t column, uint64_t size);
 void oracle_hadamard(int64_t size, float* matrix);
 void oracle_rotate(const float* x, int64_t rows, int64_t width, int64_t group, float* out);
+
+void oracle_unpack_int4(const uint8_t* packed, int64_t bytes, int8_t* out);
+float oracle_bf16_to_f32(uint16_t b);
+void oracle_w4a16_dequant(const uint8_t* packed, const uint16_t* scale_bf16, int64_t rows,
+                          int64_t width, int64_t group, int f16_round, float* w_deq);
+void oracle_w4a16_f64(const uint16_t* x, int64_t rows, int64_t width, const uint8_t* packed,
+                      const uint16_t* scale_bf16, int64_t group, const uint16_t* bias,
+                      int64_t columns, double* out);
+void oracle_w4a16_gemm(const uint16_t* x, int64_t rows, int64_t width, const uint8_t* packed,
+                       const uint16_t* scale_bf16, int64_t group, const uint16_t* bias,
+                       int64_t columns, uint16_t* out);
 
 #ifdef __cplusplus
 }

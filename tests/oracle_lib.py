@@ -42,6 +42,11 @@ class Oracle:
             "oracle_hadamard_sign_negative": (ctypes.c_int, [ctypes.c_uint64] * 3),
             "oracle_hadamard": (None, [_I, _P]),
             "oracle_rotate": (None, [_P, _I, _I, _I, _P]),
+            "oracle_unpack_int4": (None, [_P, _I, _P]),
+            "oracle_bf16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+            "oracle_w4a16_dequant": (None, [_P, _P, _I, _I, _I, ctypes.c_int, _P]),
+            "oracle_w4a16_f64": (None, [_P, _I, _I, _P, _P, _I, _P, _I, _P]),
+            "oracle_w4a16_gemm": (None, [_P, _I, _I, _P, _P, _I, _P, _I, _P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -169,3 +174,42 @@ class Oracle:
         out = np.empty_like(x)
         self.L.oracle_rotate(_p(x), rows, width, group, _p(out))
         return out
+
+    # -- W4A16 (crates/minicpm-v/src/quant.rs) --------------------------------
+    def unpack_int4(self, packed):
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        out = np.empty(packed.size * 2, dtype=np.int8)
+        self.L.oracle_unpack_int4(_p(packed), packed.size, _p(out))
+        return out
+
+    def w4a16_dequant(self, packed, scale_bf16, rows, width, group=128, f16_round=False):
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        scale_bf16 = np.ascontiguousarray(scale_bf16).view(np.uint16)
+        out = np.empty((rows, width), dtype=np.float32)
+        self.L.oracle_w4a16_dequant(_p(packed), _p(scale_bf16), rows, width, group, int(f16_round),
+                                    _p(out))
+        return out
+
+    def w4a16_f64(self, x16, packed, scale_bf16, group=128, bias16=None):
+        x16 = np.ascontiguousarray(x16).view(np.uint16)
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        scale_bf16 = np.ascontiguousarray(scale_bf16).view(np.uint16)
+        bias16 = None if bias16 is None else np.ascontiguousarray(bias16).view(np.uint16)
+        rows, width = x16.shape
+        columns = packed.shape[0]
+        out = np.empty((rows, columns), dtype=np.float64)
+        self.L.oracle_w4a16_f64(_p(x16), rows, width, _p(packed), _p(scale_bf16), group, _p(bias16),
+                                columns, _p(out))
+        return out
+
+    def w4a16_gemm(self, x16, packed, scale_bf16, group=128, bias16=None):
+        x16 = np.ascontiguousarray(x16).view(np.uint16)
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        scale_bf16 = np.ascontiguousarray(scale_bf16).view(np.uint16)
+        bias16 = None if bias16 is None else np.ascontiguousarray(bias16).view(np.uint16)
+        rows, width = x16.shape
+        columns = packed.shape[0]
+        out = np.empty((rows, columns), dtype=np.uint16)
+        self.L.oracle_w4a16_gemm(_p(x16), rows, width, _p(packed), _p(scale_bf16), group, _p(bias16),
+                                 columns, _p(out))
+        return out.view(np.float16)

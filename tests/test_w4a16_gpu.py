@@ -1,0 +1,82 @@
+"""W4A16 (MiniCPM-V pack-quantized int4, group 128, bf16 scales) on the GPU.
+
+The reference dequantises inside Burn/cubek's quantized matmul on the GPU and
+at load on the CPU (crates/minicpm-v/src/quant.rs:145-201); both are checked
+by its own test against an f64 product with a 5e-2 absolute tolerance
+(quant.rs:466-503). Here: that test's synthetic weights and shapes, and
+random cases over every kernel path (GEMV, skinny, tiled prefill) against
+the f64 truth at 1e-2 relative and the oracle's dequantise-then-dot route.
+"""
+import numpy as np
+import pytest
+import torch
+
+import omni_int8 as oi
+import tolerance
+import w4a16_data as wd
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    assert oi.arch_supported(torch.cuda.current_device()), "device is not gfx950"
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def run(x, packed, bits, b=None, group=128):
+    scale = torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).cuda()
+    y = oi.w4a16_linear(dev(x), dev(packed), scale, None if b is None else dev(b), group=group)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+@pytest.mark.parametrize("out,input,m", [(512, 2048, 21), (2048, 512, 21), (512, 2048, 1),
+                                         (512, 2048, 4), (2048, 512, 130)])
+def test_reference_synthetic_case(oracle, out, input, m):
+    packed, bits, q, scale = wd.reference_synthetic(out, input)
+    if m <= 21:
+        x = wd.reference_activations(m, input)
+    else:
+        x = np.tile(wd.reference_activations(21, input), (m // 21 + 1, 1))[:m]
+    got = run(x, packed, bits).astype(np.float64)
+    truth = oracle.w4a16_f64(x, packed, bits)
+    assert np.abs(got - truth).max() < 5e-2            # the reference's own bar
+    assert tolerance.rel_err(got, truth) <= tolerance.FP16_REL_TOL
+
+
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 16, 33, 64, 65, 300])
+@pytest.mark.parametrize("width,columns,group", [(2048, 512, 128), (512, 2048, 128), (4096, 77, 128),
+                                                 (1536, 130, 64), (96, 9, 32)])
+def test_every_path_random(oracle, rows, width, columns, group):
+    rng = np.random.default_rng(rows * 7 + width + columns + group)
+    x, packed, bits, b = wd.random_case(rng, rows, width, columns, group, bias=columns % 2 == 1)
+    got = run(x, packed, bits, b, group).astype(np.float64)
+    truth = oracle.w4a16_f64(x, packed, bits, group, b)
+    assert tolerance.rel_err(got, truth) <= tolerance.FP16_REL_TOL, (rows, width, columns, group)
+    route = oracle.w4a16_gemm(x, packed, bits, group, b).astype(np.float64)
+    assert tolerance.rel_err(got, route) <= tolerance.FP16_REL_TOL
+
+
+def test_integer_inputs_are_exact():
+    # integer x and unit scales: every partial sum is an integer below 2^11
+    x = np.tile(np.arange(-4, 4, dtype=np.float16), (3, 32))[:, :256].copy()
+    q = ((np.arange(6 * 256) % 7) - 3).reshape(6, 256)
+    bits = wd.bf16_bits(np.ones((6, 2), np.float32))
+    for rows in (3, 9, 70):
+        xr = np.tile(x, (rows // 3 + 1, 1))[:rows]
+        got = run(xr, wd.pack_int4(q), bits)
+        want = (xr.astype(np.int64) @ q.astype(np.int64).T).astype(np.float16)
+        assert np.array_equal(got, want), rows
+
+
+def test_guards():
+    x = torch.zeros((2, 200), dtype=torch.float16, device="cuda")
+    w = torch.zeros((4, 100), dtype=torch.uint8, device="cuda")
+    s = torch.zeros((4, 2), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError):
+        oi.w4a16_linear(x, w, s, group=100)   # group % 32 != 0: not handled
