@@ -184,6 +184,38 @@ def cpu_gemv_baseline(oracle, np, seconds):
                       f"{elapsed:.1f} s single-thread C restatement"}
 
 
+def w4a16_bench(torch, oi, gen, dev, stream, steps):
+    """Weight-only int4 GEMV (group 128, bf16 scales) at M=1 on the W8A16
+    headline shape K=4096, N=14336, over weight copies rotated past the MALL:
+    HBM GB/s of its algorithmic bytes (N*K/2 codes + 2*N*K/128 scales +
+    2*K activations + 2*N outputs)."""
+    M, K, N = 1, 4096, 14336
+    wbytes = N * K // 2 + 2 * N * (K // 128)
+    copies = max(4, -(-GEMV_ROTATION_BYTES // wbytes))
+    x = torch.randn((M, K), generator=gen, device=dev).half()
+    ws = [torch.randint(0, 256, (N, K // 2), generator=gen, device=dev, dtype=torch.uint8)
+          for _ in range(copies)]
+    ss = [(torch.rand((N, K // 128), generator=gen, device=dev) * 0.02 + 0.002).to(torch.bfloat16)
+          for _ in range(copies)]
+    idx = [0]
+
+    def gemv():
+        i = idx[0] % copies
+        oi.w4a16_linear(x, ws[i], ss[i])
+        idx[0] += 1
+
+    for _ in range(2 * copies):
+        gemv()
+    iters = copies * max(1, steps // 4)
+    g = graph_of(gemv, iters)
+    t = timed_graph(g, stream) / iters
+    del g
+    nbytes = wbytes + 2 * M * K + 2 * M * N
+    return {"M": M, "K": K, "N": N, "group": 128, "weight_copies": copies,
+            "us_per_launch": round(t * 1e6, 3), "GB/s": round(nbytes / t / 1e9, 1),
+            "roofline_frac": round(nbytes / t / 1e9 / PEAK_HBM_GBS, 4)}
+
+
 def convrot_bench(torch, oi, gen, dev, stream, steps):
     """BASELINE config 4 (M=4352 = 4096 image + 256 text tokens): the fused
     ConvRot rotation + quantisation of the f16 activations at widths 3072
@@ -326,6 +358,9 @@ def main():
     gemv_bytes = gN * gK + 2 * gN + 2 * gM * gK + 2 * gM * gN
     gemv_gbs = gemv_bytes / t_gemv / 1e9
 
+    # ---- W4A16 GEMV (MiniCPM-V pack-quantized int4) --------------------------
+    w4 = w4a16_bench(torch, oi, gen, dev, stream, args.steps)
+
     # ---- ConvRot: fused rotation + quantisation, and one whole layer ---------
     convrot_res = convrot_bench(torch, oi, gen, dev, stream, args.steps)
 
@@ -367,6 +402,7 @@ def main():
             "cpu_baseline": cpu_gemv,
         },
         "convrot": convrot_res,
+        "w4a16_gemv": w4,
     }
     print(json.dumps(line))
 

@@ -21,6 +21,7 @@
 //    staging it into LDS, then runs v_mfma_f32_32x32x16_f16 on LDS fragments
 //    with the same swizzled, double-buffered layout as the W8A8 kernel.
 #include <cstdlib>
+#include <type_traits>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -1010,14 +1011,25 @@ hipError_t launch_w4a16_gemv(const W8A16Args& a, hipStream_t stream) {
     const int64_t chunks = a.width / 32;
     const int64_t T = ((chunks + 63) / 64) * 64;
     if (T > 1024) return hipErrorInvalidValue;  // the caller keeps width <= 32768
-    constexpr int R = 4;
-    const dim3 grid((unsigned)((a.columns + R - 1) / R)), block((unsigned)T);
-    switch (a.rows) {
-        case 1: hipLaunchKernelGGL((w4a16_gemv_kernel<1, R>), grid, block, 0, stream, a); break;
-        case 2: hipLaunchKernelGGL((w4a16_gemv_kernel<2, R>), grid, block, 0, stream, a); break;
-        default: hipLaunchKernelGGL((w4a16_gemv_kernel<4, R>), grid, block, 0, stream, a); break;
-    }
-    return hipGetLastError();
+    // Rows per workgroup: 8 measured best on MI355X for decode shapes of tens
+    // of MB and more (2 on matrices of a few MB); OMNI_W4A16_GEMV pins it.
+    const char* ov = std::getenv("OMNI_W4A16_GEMV");
+    const int r = ov ? std::atoi(ov) : (a.columns * a.width / 2 >= (4 << 20) ? 8 : 2);
+    auto go = [&](auto rt) {
+        constexpr int R = decltype(rt)::value;
+        const dim3 grid((unsigned)((a.columns + R - 1) / R)), block((unsigned)T);
+        switch (a.rows) {
+            case 1: hipLaunchKernelGGL((w4a16_gemv_kernel<1, R>), grid, block, 0, stream, a); break;
+            case 2: hipLaunchKernelGGL((w4a16_gemv_kernel<2, R>), grid, block, 0, stream, a); break;
+            default: hipLaunchKernelGGL((w4a16_gemv_kernel<4, R>), grid, block, 0, stream, a); break;
+        }
+        return hipGetLastError();
+    };
+    if (r == 1) return go(std::integral_constant<int, 1>{});
+    if (r == 2) return go(std::integral_constant<int, 2>{});
+    if (r == 8) return go(std::integral_constant<int, 8>{});
+    if (r == 16) return go(std::integral_constant<int, 16>{});
+    return go(std::integral_constant<int, 4>{});
 }
 
 hipError_t launch_w4a16_skinny(const W8A16Args& a, hipStream_t stream) {

@@ -62,6 +62,17 @@ def test_every_path_random(oracle, rows, width, columns, group):
     assert tolerance.rel_err(got, route) <= tolerance.FP16_REL_TOL
 
 
+@pytest.mark.parametrize("r", ["1", "2", "4", "8", "16"])
+def test_gemv_every_rows_per_workgroup(oracle, monkeypatch, r):
+    monkeypatch.setenv("OMNI_W4A16_GEMV", r)
+    for rows, width, columns in ((1, 4096, 37), (4, 2048, 130), (3, 96, 9)):
+        rng = np.random.default_rng(rows + width + columns + int(r))
+        x, packed, bits, b = wd.random_case(rng, rows, width, columns, 32, bias=True)
+        got = run(x, packed, bits, b, 32).astype(np.float64)
+        truth = oracle.w4a16_f64(x, packed, bits, 32, b)
+        assert tolerance.rel_err(got, truth) <= tolerance.FP16_REL_TOL, (r, rows, width, columns)
+
+
 def test_integer_inputs_are_exact():
     # integer x and unit scales: every partial sum is an integer below 2^11
     x = np.tile(np.arange(-4, 4, dtype=np.float16), (3, 32))[:, :256].copy()
