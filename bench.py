@@ -30,6 +30,7 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 PEAK_INT8_TOPS = 5000.0     # MI355X dense int8 MFMA, 5.0 POP/s
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, 8 TB/s
+PEAK_F16_TFLOPS = 2500.0    # MI355X dense fp16 MFMA, 2.5 PFLOP/s
 GEMM_SHAPES = [(4096, 3072, 12288), (4096, 12288, 3072)]  # (M, K, N)
 GEMV_SHAPE = (1, 4096, 14336)
 GEMV_ROTATION_BYTES = 1 << 30
@@ -216,6 +217,53 @@ def w4a16_bench(torch, oi, gen, dev, stream, steps):
             "roofline_frac": round(nbytes / t / 1e9 / PEAK_HBM_GBS, 4)}
 
 
+def f16_bench(torch, gen, dev, stream, steps):
+    """The fp16 analogs: the Breeze depth GEMV at its 8192 -> 1024 projection
+    (M=1, over weight copies rotated past the MALL) in HBM GB/s of its
+    algorithmic bytes (2*N*K weights + 2*K + 2*N), and the Qwen-Image DiT GEMM
+    at 4096 x 4096 x 12288 (M x K x N) in TFLOP/s, with torch.matmul
+    (hipBLASLt) on the same operands beside it."""
+    from omni_int8.f16 import depth_try_linear, tensorops_try_linear
+    M, K, N = 1, 8192, 1024
+    wbytes = 2 * N * K
+    copies = max(4, -(-GEMV_ROTATION_BYTES // wbytes))
+    x = torch.randn((M, K), generator=gen, device=dev).half()
+    ws = [(torch.randn((N, K), generator=gen, device=dev) * 0.02).half() for _ in range(copies)]
+    idx = [0]
+
+    def gemv():
+        depth_try_linear(x, ws[idx[0] % copies].t())
+        idx[0] += 1
+
+    for _ in range(2 * copies):
+        gemv()
+    iters = copies * max(1, steps // 4)
+    g = graph_of(gemv, iters)
+    t = timed_graph(g, stream) / iters
+    del g
+    nbytes = wbytes + 2 * M * K + 2 * M * N
+    res = {"depth_gemv": {"M": M, "K": K, "N": N, "weight_copies": copies,
+                          "us_per_launch": round(t * 1e6, 3), "GB/s": round(nbytes / t / 1e9, 1),
+                          "roofline_frac": round(nbytes / t / 1e9 / PEAK_HBM_GBS, 4)}}
+    M, K, N = 4096, 4096, 12288
+    x = torch.randn((M, K), generator=gen, device=dev).half()
+    w = (torch.randn((N, K), generator=gen, device=dev) * 0.02).half()
+    wt = w.t()
+    flops = 2.0 * M * N * K
+    times = {}
+    for name, fn in (("omni", lambda: tensorops_try_linear(x, wt)), ("torch_matmul", lambda: x @ wt)):
+        for _ in range(3):
+            fn()
+        g = graph_of(fn, steps)
+        times[name] = timed_graph(g, stream) / steps
+        del g
+    res["dit_gemm"] = {"M": M, "K": K, "N": N, "us": round(times["omni"] * 1e6, 2),
+                       "TFLOP/s": round(flops / times["omni"] / 1e12, 1),
+                       "roofline_frac": round(flops / times["omni"] / 1e12 / PEAK_F16_TFLOPS, 4),
+                       "torch_matmul_TFLOP/s": round(flops / times["torch_matmul"] / 1e12, 1)}
+    return res
+
+
 def convrot_bench(torch, oi, gen, dev, stream, steps):
     """BASELINE config 4 (M=4352 = 4096 image + 256 text tokens): the fused
     ConvRot rotation + quantisation of the f16 activations at widths 3072
@@ -361,6 +409,9 @@ def main():
     # ---- W4A16 GEMV (MiniCPM-V pack-quantized int4) --------------------------
     w4 = w4a16_bench(torch, oi, gen, dev, stream, args.steps)
 
+    # ---- fp16 analogs: depth GEMV and DiT GEMM -------------------------------
+    f16_res = f16_bench(torch, gen, dev, stream, args.steps)
+
     # ---- ConvRot: fused rotation + quantisation, and one whole layer ---------
     convrot_res = convrot_bench(torch, oi, gen, dev, stream, args.steps)
 
@@ -403,6 +454,7 @@ def main():
         },
         "convrot": convrot_res,
         "w4a16_gemv": w4,
+        "f16": f16_res,
     }
     print(json.dumps(line))
 

@@ -179,6 +179,30 @@ int omni_w4a16_gemm(const uint16_t* x, const uint8_t* w_packed, const uint16_t* 
                     int64_t group, const uint16_t* bias, int64_t rows, int64_t columns,
                     int64_t width, uint16_t* out, void* stream);
 
+/* fp16 decode GEMV, the Breeze TTS depth decoder's linear. Replaces
+ * crates/breeze-tts/src/metal_depth.rs:84-123 (try_linear) and the kernel it
+ * launches (gemv_kernel :13-35 via raw_gemv :36-83):
+ *   out[m][n] = f16(sum_k f32(x[m][k]) * f32(w[n][k]))
+ * x f16 [rows][width], w f16 [columns][width] (output-major: the transposed
+ * view of the Linear's [width][columns] weight that the reference's custom
+ * path takes, :42-44), out f16 [rows][columns]. f32 accumulation; the
+ * summation order is not the reference's. The reference's guard (:94-104):
+ * 1 <= rows <= 64, width > 0, width % 32 == 0, 1 <= columns <= 4096, else
+ * OMNI_NOT_HANDLED (its None). x and w 16-byte aligned. */
+int omni_f16_gemv(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t columns,
+                  int64_t width, uint16_t* out, void* stream);
+
+/* fp16 GEMM for the Qwen-Image DiT linears. Replaces
+ * crates/qwen-image/src/metal_tensorops.rs:161-203 (try_linear) and its
+ * 64 x 64 matmul2d shader (tensorops.metal:18-39): out = f16(x @ w^T) with
+ * f32 accumulation, x f16 [rows][width], w f16 [columns][width], out f16
+ * [rows][columns]. The reference's guard (:174-187): 256 <= rows <= 65535,
+ * width and columns multiples of 64 in 4096..=12288, else OMNI_NOT_HANDLED;
+ * OMNI_QWEN_TENSOROPS=0 in the environment (read once) turns it off, as
+ * :165-169 does. x and w 16-byte aligned. */
+int omni_f16_gemm(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t columns,
+                  int64_t width, uint16_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -113,6 +113,41 @@ int run_w8a8(const int32_t* x_packed, const float* x_scale, const int32_t* x_sum
     return hip_status(omni::launch_w8a8_scalar(a, stream), "w8a8 scalar launch");
 }
 
+// Shared body of the two fp16 linears once the reference's guard has passed.
+int f16_linear(const char* name, const uint16_t* x, const uint16_t* w, int64_t rows,
+               int64_t columns, int64_t width, uint16_t* out, void* stream) {
+    if (!x || !w || !out) return fail(OMNI_BAD_ARGUMENT, "%s: null pointer", name);
+    if (!aligned(x, 16) || !aligned(w, 16))
+        return fail(OMNI_BAD_ARGUMENT, "%s: x and w must be 16-byte aligned", name);
+    int st = check_current_device();
+    if (st != OMNI_OK) return st;
+    omni::W8A16Args a;
+    a.x = reinterpret_cast<const _Float16*>(x);
+    a.w = reinterpret_cast<const int8_t*>(w);
+    a.scale = nullptr;
+    a.bias = nullptr;
+    a.out = reinterpret_cast<_Float16*>(out);
+    a.rows = rows;
+    a.columns = columns;
+    a.width = width;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // The GEMV gives a row to one workgroup of at most 1024 lanes with up to
+    // four 8-element chunks each: width <= 32768.
+    if (rows <= 4 && width <= 32768) return hip_status(omni::launch_f16_gemv(a, s), "f16 gemv launch");
+    if (rows <= 64) return hip_status(omni::launch_f16_skinny(a, s), "f16 skinny launch");
+    return hip_status(omni::launch_f16_mfma(a, s), "f16 mfma launch");
+}
+
+// OMNI_QWEN_TENSOROPS=0 turns omni_f16_gemm off (NOT_HANDLED), read once per
+// process as crates/qwen-image/src/metal_tensorops.rs:165-169 reads it.
+bool qwen_tensorops_enabled() {
+    static const bool value = [] {
+        const char* v = std::getenv("OMNI_QWEN_TENSOROPS");
+        return !(v && std::strcmp(v, "0") == 0);
+    }();
+    return value;
+}
+
 }  // namespace
 
 extern "C" {
@@ -351,6 +386,26 @@ int omni_w4a16_gemm(const uint16_t* x, const uint8_t* w_packed, const uint16_t* 
         return hip_status(omni::launch_w4a16_gemv(a, s), "w4a16 gemv launch");
     if (rows <= 64) return hip_status(omni::launch_w4a16_skinny(a, s), "w4a16 skinny launch");
     return hip_status(omni::launch_w4a16_mfma(a, s), "w4a16 mfma launch");
+}
+
+int omni_f16_gemv(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t columns,
+                  int64_t width, uint16_t* out, void* stream) {
+    // crates/breeze-tts/src/metal_depth.rs:94-104
+    if (rows < 1 || rows > 64 || width <= 0 || width % 32 != 0 || columns <= 0 || columns > 4096)
+        return fail(OMNI_NOT_HANDLED, "f16_gemv: rows %lld, width %lld, columns %lld outside 1..=64, "
+                    "width %% 32 == 0, 1..=4096", (long long)rows, (long long)width, (long long)columns);
+    return f16_linear("f16_gemv", x, w, rows, columns, width, out, stream);
+}
+
+int omni_f16_gemm(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t columns,
+                  int64_t width, uint16_t* out, void* stream) {
+    if (!qwen_tensorops_enabled()) return fail(OMNI_NOT_HANDLED, "f16_gemm: OMNI_QWEN_TENSOROPS=0");
+    // crates/qwen-image/src/metal_tensorops.rs:174-187
+    if (rows < 256 || rows > 65535 || width % 64 != 0 || columns % 64 != 0 || width < 4096 ||
+        columns < 4096 || width > 12288 || columns > 12288)
+        return fail(OMNI_NOT_HANDLED, "f16_gemm: rows %lld, width %lld, columns %lld outside 256..=65535, "
+                    "4096..=12288 in steps of 64", (long long)rows, (long long)width, (long long)columns);
+    return f16_linear("f16_gemm", x, w, rows, columns, width, out, stream);
 }
 
 }  // extern "C"

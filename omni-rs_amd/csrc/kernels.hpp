@@ -35,7 +35,7 @@ hipError_t launch_w8a8_scalar(const W8A8Args& a, hipStream_t stream);
 
 struct W8A16Args {
     const _Float16* x;      // [rows][width]
-    const int8_t* w;        // [columns][width] int8, or [columns][width / 2] packed int4
+    const int8_t* w;        // [columns][width] int8, [columns][width / 2] packed int4, or f16
     const _Float16* scale;  // [columns] (int8 weights)
     const _Float16* bias;   // [columns] or null
     _Float16* out;          // [rows][columns]
@@ -53,5 +53,11 @@ hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream);
 hipError_t launch_w4a16_gemv(const W8A16Args& a, hipStream_t stream);
 hipError_t launch_w4a16_skinny(const W8A16Args& a, hipStream_t stream);
 hipError_t launch_w4a16_mfma(const W8A16Args& a, hipStream_t stream);
+
+// fp16 linear (w8a16.hip): w is f16 [columns][width] (cast to int8_t*), no
+// scale; out[m][n] = f16(sum_k x[m][k] * w[n][k] + bias[n]).
+hipError_t launch_f16_gemv(const W8A16Args& a, hipStream_t stream);
+hipError_t launch_f16_skinny(const W8A16Args& a, hipStream_t stream);
+hipError_t launch_f16_mfma(const W8A16Args& a, hipStream_t stream);
 
 }  // namespace omni

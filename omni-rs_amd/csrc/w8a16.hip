@@ -125,45 +125,53 @@ __device__ __forceinline__ int fold_index(int lane) {
 
 // MR activation rows (1, 2 or 4; unused rows are zero). A workgroup of T
 // lanes (T = blockDim.x, a multiple of 64, at most 1024) owns R consecutive
-// weight rows; lane t owns the 16-element k chunks t + T*j, j < CPL, so one
-// row of W is T*CPL*16 bytes wide at most. Every weight load of the
-// workgroup is issued before any arithmetic (after x's chunks, which hit in
-// L2), as nontemporal loads (the weights are read once; keeping them out of
-// the caches keeps x and the scales there), so the whole workgroup's share
-// of W is in flight at once. One workgroup per row group, many of them
-// resident per CU, keeps the HBM queues full: measured on MI355X this
-// streams within a few percent of a bare read kernel of the same size, and
-// a 525 MB weight (a 128256 x 4096 vocabulary head) at 7.2 TB/s.
-template <int MR, int CPL, int R>
+// weight rows; lane t owns the 16-byte weight chunks t + T*j, j < CPL (16
+// int8 codes, or 8 halves with WB = 16), so one row of W is T*CPL*16 bytes
+// wide at most. Every weight load of the workgroup is issued before any
+// arithmetic (after x's chunks, which hit in L2), as nontemporal loads (the
+// weights are read once; keeping them out of the caches keeps x and the
+// scales there), so the whole workgroup's share of W is in flight at once.
+// One workgroup per row group, many of them resident per CU, keeps the HBM
+// queues full: measured on MI355X this streams within a few percent of a
+// bare read kernel of the same size, and a 525 MB weight (a 128256 x 4096
+// vocabulary head) at 7.2 TB/s.
+// WB = 16: f16 weights, no scale (the fp16 linear).
+template <int MR, int CPL, int R, int WB = 8>
 __global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
     constexpr int V = R * MR;
     static_assert((V & (V - 1)) == 0 && V <= 64, "power-of-two partial count");
+    static_assert(WB == 8 || WB == 16, "int8 or f16 weights");
+    constexpr int kE = WB == 8 ? 16 : 8;  // weights per 16-byte chunk
+    constexpr int kP = kE / 2;            // f16 pairs of x per chunk
     __shared__ float s_part[16][V];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int T = blockDim.x;
     const int64_t K = a.width;
-    const int64_t chunks = K / 16;
+    const int64_t chunks = K / kE;
     const int64_t n0 = (int64_t)blockIdx.x * R;
 
-    // x chunks: 16 halves of each owned chunk and row as 8 f16 pairs.
-    v2h xr[CPL][MR][8];
+    // x chunks: kE halves of each owned chunk and row as kP f16 pairs.
+    v2h xr[CPL][MR][kP];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
         const int64_t c = tid + (int64_t)T * j;
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
             if (c < chunks && m < a.rows) {
-                const uint4* p = reinterpret_cast<const uint4*>(a.x + m * K + c * 16);
-                const uint4 q0 = p[0], q1 = p[1];
-                xr[j][m][0] = bits_half2(q0.x); xr[j][m][1] = bits_half2(q0.y);
-                xr[j][m][2] = bits_half2(q0.z); xr[j][m][3] = bits_half2(q0.w);
-                xr[j][m][4] = bits_half2(q1.x); xr[j][m][5] = bits_half2(q1.y);
-                xr[j][m][6] = bits_half2(q1.z); xr[j][m][7] = bits_half2(q1.w);
+                const uint4* p = reinterpret_cast<const uint4*>(a.x + m * K + c * kE);
+#pragma unroll
+                for (int u = 0; u < kE / 8; ++u) {
+                    const uint4 q = p[u];
+                    xr[j][m][4 * u] = bits_half2(q.x);
+                    xr[j][m][4 * u + 1] = bits_half2(q.y);
+                    xr[j][m][4 * u + 2] = bits_half2(q.z);
+                    xr[j][m][4 * u + 3] = bits_half2(q.w);
+                }
             } else {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) xr[j][m][e] = v2h{};
+                for (int e = 0; e < kP; ++e) xr[j][m][e] = v2h{};
             }
         }
     }
@@ -176,7 +184,7 @@ __global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int64_t n = n0 + r < a.columns ? n0 + r : a.columns - 1;
-        const int8_t* wrow = a.w + n * K;
+        const uint8_t* wrow = reinterpret_cast<const uint8_t*>(a.w) + n * K * (WB / 8);
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const int64_t c = tid + (int64_t)T * j < chunks ? tid + (int64_t)T * j : chunks - 1;
@@ -185,8 +193,13 @@ __global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
     }
     // This thread's epilogue row (tid / MR) % R: scale and bias.
     const int64_t n_ep = min(n0 + (tid / MR) % R, a.columns - 1);
-    const _Float16 sc_h = a.scale[n_ep];
-    const _Float16 bi_h = (a.bias ? a.bias : a.scale)[n_ep];  // unconditional load
+    _Float16 sc_h = (_Float16)1.0f, bi_h = (_Float16)0.0f;
+    if constexpr (WB == 8) {
+        sc_h = a.scale[n_ep];
+        bi_h = (a.bias ? a.bias : a.scale)[n_ep];  // unconditional load
+    } else {
+        if (a.bias) bi_h = a.bias[n_ep];
+    }
 
     float part[V];
 #pragma unroll
@@ -198,13 +211,21 @@ __global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
             const u32 words[4] = {wv[r][j].x, wv[r][j].y, wv[r][j].z, wv[r][j].w};
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                v2h w01, w23;
-                i8x4_to_f16x4(words[q], w01, w23);
+                if constexpr (WB == 8) {
+                    v2h w01, w23;
+                    i8x4_to_f16x4(words[q], w01, w23);
 #pragma unroll
-                for (int m = 0; m < MR; ++m) {
-                    float& p = part[r * MR + m];
-                    p = __builtin_amdgcn_fdot2(w01, xr[j][m][2 * q], p, false);
-                    p = __builtin_amdgcn_fdot2(w23, xr[j][m][2 * q + 1], p, false);
+                    for (int m = 0; m < MR; ++m) {
+                        float& p = part[r * MR + m];
+                        p = __builtin_amdgcn_fdot2(w01, xr[j][m][2 * q], p, false);
+                        p = __builtin_amdgcn_fdot2(w23, xr[j][m][2 * q + 1], p, false);
+                    }
+                } else {
+#pragma unroll
+                    for (int m = 0; m < MR; ++m) {
+                        float& p = part[r * MR + m];
+                        p = __builtin_amdgcn_fdot2(bits_half2(words[q]), xr[j][m][q], p, false);
+                    }
                 }
             }
         }
@@ -225,46 +246,57 @@ __global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
 }
 
 // OMNI_W8A16_GEMV=<cpl><r> (e.g. 14 = one chunk per lane, four rows per
-// workgroup) pins the GEMV configuration (tuning aid; unset = heuristic).
-// Read on every launch so one process can time each configuration.
-int gemv_cfg_override() {
-    const char* v = std::getenv("OMNI_W8A16_GEMV");
+// workgroup) pins the int8 GEMV configuration, OMNI_F16_GEMV the f16 one
+// (tuning aids; unset = heuristic). Read on every launch so one process can
+// time each configuration.
+int gemv_cfg_override(int wb) {
+    const char* v = std::getenv(wb == 8 ? "OMNI_W8A16_GEMV" : "OMNI_F16_GEMV");
     return v ? std::atoi(v) : 0;
 }
 
-template <int MR, int CPL, int R>
+template <int MR, int CPL, int R, int WB>
 hipError_t launch_gemv_cfg(const W8A16Args& a, hipStream_t stream) {
-    const int64_t chunks = a.width / 16;
+    const int64_t chunks = a.width / (WB == 8 ? 16 : 8);
     const int64_t lanes = (chunks + CPL - 1) / CPL;
     const int64_t T = ((lanes + 63) / 64) * 64;
-    if (T > 1024) return hipErrorInvalidValue;  // the caller keeps width <= 16384
+    if (T > 1024) return hipErrorInvalidValue;  // the caller bounds width
     const int64_t grid = (a.columns + R - 1) / R;
-    hipLaunchKernelGGL((w8a16_gemv_kernel<MR, CPL, R>), dim3((unsigned)grid), dim3((unsigned)T), 0,
+    hipLaunchKernelGGL((w8a16_gemv_kernel<MR, CPL, R, WB>), dim3((unsigned)grid), dim3((unsigned)T), 0,
                        stream, a);
     return hipGetLastError();
 }
 
-template <int MR>
+template <int MR, int WB>
 hipError_t launch_gemv_m(const W8A16Args& a, hipStream_t stream) {
-    switch (gemv_cfg_override()) {
-        case 11: return launch_gemv_cfg<MR, 1, 1>(a, stream);
-        case 12: return launch_gemv_cfg<MR, 1, 2>(a, stream);
-        case 14: return launch_gemv_cfg<MR, 1, 4>(a, stream);
-        case 18: return launch_gemv_cfg<MR, 1, 8>(a, stream);
-        case 21: return launch_gemv_cfg<MR, 2, 1>(a, stream);
-        case 22: return launch_gemv_cfg<MR, 2, 2>(a, stream);
-        case 24: return launch_gemv_cfg<MR, 2, 4>(a, stream);
+    switch (gemv_cfg_override(WB)) {
+        case 11: return launch_gemv_cfg<MR, 1, 1, WB>(a, stream);
+        case 12: return launch_gemv_cfg<MR, 1, 2, WB>(a, stream);
+        case 14: return launch_gemv_cfg<MR, 1, 4, WB>(a, stream);
+        case 18: return launch_gemv_cfg<MR, 1, 8, WB>(a, stream);
+        case 21: return launch_gemv_cfg<MR, 2, 1, WB>(a, stream);
+        case 22: return launch_gemv_cfg<MR, 2, 2, WB>(a, stream);
+        case 24: return launch_gemv_cfg<MR, 2, 4, WB>(a, stream);
+        case 41: return launch_gemv_cfg<MR, 4, 1, WB>(a, stream);
         default: break;
+    }
+    const int64_t chunks = a.width / (WB == 8 ? 16 : 8);
+    if constexpr (WB == 16) {
+        // f16 weights: 2048 chunks (K = 16384) fit one chunk each of 1024
+        // lanes twice over; wider rows take four chunks per lane.
+        if (chunks > 2048) return launch_gemv_cfg<MR, 4, 1, WB>(a, stream);
+        if (chunks > 1024) return launch_gemv_cfg<MR, 2, 2, WB>(a, stream);
+        if (a.columns * a.width * 2 <= (4 << 20)) return launch_gemv_cfg<MR, 1, 2, WB>(a, stream);
+        if (MR == 4) return launch_gemv_cfg<MR, 1, 8, WB>(a, stream);
+        return launch_gemv_cfg<MR, 1, 4, WB>(a, stream);
     }
     // Measured on MI355X over the BASELINE decode shapes: 64 bytes of weights
     // in flight per lane (128 with four activation rows), two chunks per
     // lane once a row is wider than 512 chunks, and more, smaller
     // workgroups when the whole matrix is a few MB.
-    const int64_t chunks = a.width / 16;
-    if (a.columns * a.width <= (4 << 20)) return launch_gemv_cfg<MR, 2, 1>(a, stream);
-    if (chunks > 512) return launch_gemv_cfg<MR, 2, 4>(a, stream);
-    if (MR == 4) return launch_gemv_cfg<MR, 1, 8>(a, stream);
-    return launch_gemv_cfg<MR, 1, 4>(a, stream);
+    if (a.columns * a.width <= (4 << 20)) return launch_gemv_cfg<MR, 2, 1, WB>(a, stream);
+    if (chunks > 512) return launch_gemv_cfg<MR, 2, 4, WB>(a, stream);
+    if (MR == 4) return launch_gemv_cfg<MR, 1, 8, WB>(a, stream);
+    return launch_gemv_cfg<MR, 1, 4, WB>(a, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -283,7 +315,8 @@ typedef float v4f_t __attribute__((ext_vector_type(4)));
 // B use the same lane-to-k map, so each product pairs matching k and the 64
 // k of the step are summed exactly once. The 16 waves' 16 x 16 partial tiles
 // are reduced through LDS; scale (and bias) are applied once per output.
-template <int MB>
+// WB = 16: f16 weights (32 bytes per lane per step), no scale.
+template <int MB, int WB = 8>
 __global__ __launch_bounds__(1024) void w8a16_skinny_kernel(W8A16Args a) {
     __shared__ float s_part[16][MB][256];
     const int tid = threadIdx.x;
@@ -293,7 +326,7 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_kernel(W8A16Args a) {
     const int64_t n0 = (int64_t)blockIdx.x * 16;
     const int r16 = lane & 15, g = lane >> 4;
     const int64_t wn = n0 + r16 < a.columns ? n0 + r16 : a.columns - 1;  // clamped: never stored
-    const int8_t* wrow = a.w + wn * K;
+    const uint8_t* wrow = reinterpret_cast<const uint8_t*>(a.w) + wn * K * (WB / 8);
     const _Float16* xrow[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
@@ -307,11 +340,13 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_kernel(W8A16Args a) {
     auto step = [&](int64_t st) {
         const int64_t k = st * 64 + 16 * g;
         typedef unsigned v4u __attribute__((ext_vector_type(4)));
-        v4u wv = v4u{0u, 0u, 0u, 0u};
+        v4u wv[WB / 8];
         uint4 xv[MB][2];
         // K % 16 == 0: a lane's 16-element block is wholly inside or outside.
         if (k < K) {
-            wv = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wrow + k));
+#pragma unroll
+            for (int u = 0; u < WB / 8; ++u)
+                wv[u] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wrow + k * (WB / 8)) + u);
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
                 xv[mb][0] = reinterpret_cast<const uint4*>(xrow[mb] + k)[0];
@@ -319,15 +354,23 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_kernel(W8A16Args a) {
             }
         } else {
 #pragma unroll
+            for (int u = 0; u < WB / 8; ++u) wv[u] = v4u{0u, 0u, 0u, 0u};
+#pragma unroll
             for (int mb = 0; mb < MB; ++mb) xv[mb][0] = xv[mb][1] = make_uint4(0, 0, 0, 0);
         }
-        v2h h[8];
-        i8x4_to_f16x4(wv.x, h[0], h[1]);
-        i8x4_to_f16x4(wv.y, h[2], h[3]);
-        i8x4_to_f16x4(wv.z, h[4], h[5]);
-        i8x4_to_f16x4(wv.w, h[6], h[7]);
-        const v8h b0 = {h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
-        const v8h b1 = {h[4][0], h[4][1], h[5][0], h[5][1], h[6][0], h[6][1], h[7][0], h[7][1]};
+        v8h b0, b1;
+        if constexpr (WB == 8) {
+            v2h h[8];
+            i8x4_to_f16x4(wv[0].x, h[0], h[1]);
+            i8x4_to_f16x4(wv[0].y, h[2], h[3]);
+            i8x4_to_f16x4(wv[0].z, h[4], h[5]);
+            i8x4_to_f16x4(wv[0].w, h[6], h[7]);
+            b0 = v8h{h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
+            b1 = v8h{h[4][0], h[4][1], h[5][0], h[5][1], h[6][0], h[6][1], h[7][0], h[7][1]};
+        } else {
+            __builtin_memcpy(&b0, &wv[0], 16);
+            __builtin_memcpy(&b1, &wv[WB / 8 - 1], 16);
+        }
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
             v8h a0, a1;
@@ -358,16 +401,26 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_kernel(W8A16Args a) {
 #pragma unroll
             for (int w = 0; w < 16; ++w) sum += s_part[w][mb][e];
             const float bi = a.bias ? (float)a.bias[n] : 0.0f;
-            a.out[m * a.columns + n] = (_Float16)(sum * (float)a.scale[n] + bi);
+            const float sc = WB == 8 ? (float)a.scale[n] : 1.0f;
+            a.out[m * a.columns + n] = (_Float16)(sum * sc + bi);
         }
     }
 }
 
-template <int MB>
+template <int MB, int WB>
 hipError_t launch_skinny_cfg(const W8A16Args& a, hipStream_t stream) {
     const int64_t grid = (a.columns + 15) / 16;
-    hipLaunchKernelGGL((w8a16_skinny_kernel<MB>), dim3((unsigned)grid), dim3(1024), 0, stream, a);
+    hipLaunchKernelGGL((w8a16_skinny_kernel<MB, WB>), dim3((unsigned)grid), dim3(1024), 0, stream, a);
     return hipGetLastError();
+}
+
+template <int WB>
+hipError_t launch_skinny(const W8A16Args& a, hipStream_t stream) {
+    if (a.rows == 0 || a.columns == 0) return hipSuccess;
+    if (a.rows <= 16) return launch_skinny_cfg<1, WB>(a, stream);
+    if (a.rows <= 32) return launch_skinny_cfg<2, WB>(a, stream);
+    if (a.rows <= 48) return launch_skinny_cfg<3, WB>(a, stream);
+    return launch_skinny_cfg<4, WB>(a, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -550,7 +603,8 @@ __device__ __forceinline__ int xcd_remap16(int b, int total) {
 
 // Tile rows hold BK f16 = 2*BK bytes; 16-byte chunks swizzled by row.
 // WBITS 8: int8 weights, per-column f16 scale in the epilogue; WBITS 4:
-// packed int4 weights dequantised to f16(q * s) per K group while staged.
+// packed int4 weights dequantised to f16(q * s) per K group while staged;
+// WBITS 16: f16 weights staged as they are (the fp16 linear), no scale.
 template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int GROUP_M, int WBITS = 8>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a16_mfma_kernel(W8A16Args a) {
     constexpr int kThreads = 64 * WAVES_M * WAVES_N;
@@ -560,9 +614,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a16_mfma_kernel(W
     constexpr int kChunks = kRowBytes / 16;  // 16-byte chunks (8 halves) per row
     static_assert(kChunks == 8, "BK = 64 halves");
     constexpr int kALoads = BM * kChunks / kThreads;        // x: 8 halves per load
-    constexpr int kBLoads = BN * (BK / 16) / kThreads;      // w: 16 codes per load
+    constexpr int kBPer = WBITS == 16 ? 8 : 16;             // weights per B load
+    constexpr int kBLoads = BN * (BK / kBPer) / kThreads;
     static_assert(kALoads * kThreads == BM * kChunks, "even A loads");
-    static_assert(kBLoads * kThreads == BN * (BK / 16), "even B loads");
+    static_assert(kBLoads * kThreads == BN * (BK / kBPer), "even B loads");
 
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint8_t* sA = smem;
@@ -599,9 +654,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a16_mfma_kernel(W
 #pragma unroll
         for (int i = 0; i < kBLoads; ++i) {
             const int id = tid + i * kThreads;
-            const int r = id / (BK / 16), c = id % (BK / 16);
-            const int64_t gr = n0 + r, gk = k0 + c * 16;
-            if constexpr (WBITS == 8) {
+            const int r = id / (BK / kBPer), c = id % (BK / kBPer);
+            const int64_t gr = n0 + r, gk = k0 + c * kBPer;
+            if constexpr (WBITS == 16) {
+                const _Float16* wh = reinterpret_cast<const _Float16*>(a.w);
+                rb[i] = (gr < a.columns && gk < K) ? *reinterpret_cast<const uint4*>(wh + gr * K + gk)
+                                                   : make_uint4(0, 0, 0, 0);
+            } else if constexpr (WBITS == 8) {
                 rb[i] = (gr < a.columns && gk < K) ? *reinterpret_cast<const uint4*>(a.w + gr * K + gk)
                                                    : make_uint4(0, 0, 0, 0);
             } else {
@@ -627,20 +686,24 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a16_mfma_kernel(W
 #pragma unroll
         for (int i = 0; i < kBLoads; ++i) {
             const int id = tid + i * kThreads;
-            const int r = id / (BK / 16), c = id % (BK / 16);
-            // 16 codes -> 16 halves = two 16-byte chunks 2c and 2c+1.
-            v2h h[8];
-            if constexpr (WBITS == 8) {
-                const u32 words[4] = {rb[i].x, rb[i].y, rb[i].z, rb[i].w};
-#pragma unroll
-                for (int q = 0; q < 4; ++q) i8x4_to_f16x4(words[q], h[2 * q], h[2 * q + 1]);
+            const int r = id / (BK / kBPer), c = id % (BK / kBPer);
+            if constexpr (WBITS == 16) {
+                *reinterpret_cast<uint4*>(dB + r * kRowBytes + swz(r, c) * 16) = rb[i];
             } else {
-                i4x16_dequant(rb[i].x, rb[i].y, (_Float16)bf16_to_f32((uint16_t)rb[i].z), h);
+                // 16 codes -> 16 halves = two 16-byte chunks 2c and 2c+1.
+                v2h h[8];
+                if constexpr (WBITS == 8) {
+                    const u32 words[4] = {rb[i].x, rb[i].y, rb[i].z, rb[i].w};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) i8x4_to_f16x4(words[q], h[2 * q], h[2 * q + 1]);
+                } else {
+                    i4x16_dequant(rb[i].x, rb[i].y, (_Float16)bf16_to_f32((uint16_t)rb[i].z), h);
+                }
+                uint4 lo = make_uint4(half2_bits(h[0]), half2_bits(h[1]), half2_bits(h[2]), half2_bits(h[3]));
+                uint4 hi = make_uint4(half2_bits(h[4]), half2_bits(h[5]), half2_bits(h[6]), half2_bits(h[7]));
+                *reinterpret_cast<uint4*>(dB + r * kRowBytes + swz(r, 2 * c) * 16) = lo;
+                *reinterpret_cast<uint4*>(dB + r * kRowBytes + swz(r, 2 * c + 1) * 16) = hi;
             }
-            uint4 lo = make_uint4(half2_bits(h[0]), half2_bits(h[1]), half2_bits(h[2]), half2_bits(h[3]));
-            uint4 hi = make_uint4(half2_bits(h[4]), half2_bits(h[5]), half2_bits(h[6]), half2_bits(h[7]));
-            *reinterpret_cast<uint4*>(dB + r * kRowBytes + swz(r, 2 * c) * 16) = lo;
-            *reinterpret_cast<uint4*>(dB + r * kRowBytes + swz(r, 2 * c + 1) * 16) = hi;
         }
     };
 
@@ -687,7 +750,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a16_mfma_kernel(W
     for (int j = 0; j < FN; ++j) {
         const int64_t col = n0 + wn * WN + j * 32 + (lane & 31);
         if (col >= a.columns) continue;
-        const float sc = WBITS == 8 ? (float)a.scale[col] : 1.0f;  // int4: scaled per group already
+        // int4: scaled per group already; f16: no scale
+        const float sc = WBITS == 8 ? (float)a.scale[col] : 1.0f;
         const float bias = a.bias ? (float)a.bias[col] : 0.0f;
 #pragma unroll
         for (int i = 0; i < FM; ++i)
@@ -718,16 +782,23 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a16_mfma_kernel(W
 // and one subtract, as in the GEMV). The schedule is the W8A8 ring's: one
 // fragment read and one copy behind each MFMA, one barrier per K tile between
 // the two pairs, the next tile's first copies issued before the epilogue.
-template <int BM, int BN>
+//
+// WB = 16 (the fp16 linear): W is f16 and staged like x, as two [BN][64-byte]
+// halves, and its fragments are read like x's (two ds_read_b128 per pair);
+// there is no scale.
+template <int BM, int BN, int WB = 8>
 __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     constexpr int S = 3;
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int FM = WM / 32, FN = WN / 32;
-    constexpr int kRows = 2 * BM + BN;        // 64-byte stage rows: x k 0..31, x k 32..63, W
+    constexpr int kWH = WB / 8;               // 64-byte W rows per column per K tile
+    constexpr int kRows = 2 * BM + kWH * BN;  // 64-byte stage rows: x k 0..31, x k 32..63, W
     constexpr int kStage = kRows * 64;
     constexpr int kCpw = kRows / 64;          // 1 KiB copies per wave per K tile
-    constexpr int kFrags = 2 * FM + FN;       // fragment reads per pair
+    constexpr int kFrags = 2 * FM + kWH * FN; // fragment reads per pair
     static_assert(kRows % 64 == 0 && FM >= 1 && FN >= 1, "tile shape");
+    static_assert(kCpw <= 2 * FM * FN && kFrags <= 2 * FM * FN, "one read and copy per MFMA slot");
+    static_assert(3 * kStage + 4 * BN * 4 <= 160 * 1024, "LDS");
     __shared__ __attribute__((aligned(1024))) uint8_t st0[kStage];
     __shared__ __attribute__((aligned(1024))) uint8_t st1[kStage];
     __shared__ __attribute__((aligned(1024))) uint8_t st2[kStage];
@@ -752,7 +823,7 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     const int cp_row = lane >> 2;
     const int cp_chunk = (lane & 3) ^ ((lane >> 4) & 3);
     const uint8_t* src[kCpw];
-    int adv[kCpw];  // bytes per K tile: 128 for x rows (64 halves), 64 for W rows
+    int adv[kCpw];  // bytes per K tile: 128 for x and f16 W rows (64 halves), 64 for int8 W rows
     int64_t m0 = 0, n0 = 0;
     float p_sc = 0.0f, p_bi = 0.0f;
     auto tile_origin = [&](int l, int64_t& tm0, int64_t& tn0) {
@@ -772,16 +843,18 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
                 src[j] = reinterpret_cast<const uint8_t*>(a.x + row * K) + half * 64 + cp_chunk * 16;
                 adv[j] = 128;
             } else {
-                const int64_t row = min(n0 + (c16 - 2 * BM) + cp_row, a.columns - 1);
-                src[j] = reinterpret_cast<const uint8_t*>(a.w + row * K) + cp_chunk * 16;
-                adv[j] = 64;
+                const int rel = c16 - 2 * BM;
+                const int half = WB == 16 && rel >= BN;
+                const int64_t row = min(n0 + (rel - half * BN) + cp_row, a.columns - 1);
+                src[j] = reinterpret_cast<const uint8_t*>(a.w) + row * K * kWH + half * 64 + cp_chunk * 16;
+                adv[j] = 64 * kWH;
             }
         }
     };
     auto load_params = [&](int64_t pn0) {
         if (tid < BN) {
             const int64_t col = min(pn0 + tid, a.columns - 1);
-            p_sc = (float)a.scale[col];
+            p_sc = WB == 8 ? (float)a.scale[col] : 1.0f;
             p_bi = has_bias ? (float)a.bias[col] : 0.0f;
         }
     };
@@ -804,27 +877,41 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     const int fr = lane & 31, fh = lane >> 5, fq = (fr >> 2) & 3;
     auto offA = [&](int p, int j) { return (p * BM + wm * WM + fr) * 64 + (((2 * fh + j) ^ fq) << 4); };
     auto offB = [&](int p) { return (2 * BM + wn * WN + fr) * 64 + (((2 * p + fh) ^ fq) << 4); };
-    v4i xa0[FM][2], xb0[FN], xa1[FM][2], xb1[FN];
-    // Fragment idx of a pair: A (i, j) for idx < 2 FM, else B idx - 2 FM.
-    auto read_frag = [&](int s, int p, int idx, v4i (&xa)[FM][2], v4i (&xb)[FN]) {
-        if (idx < 2 * FM)
+    auto offB16 = [&](int p, int j) {
+        return (2 * BM + p * BN + wn * WN + fr) * 64 + (((2 * fh + j) ^ fq) << 4);
+    };
+    v4i xa0[FM][2], xb0[FN][kWH], xa1[FM][2], xb1[FN][kWH];
+    // Fragment idx of a pair: A (i, j) for idx < 2 FM, else B idx - 2 FM
+    // (int8: column block idx - 2 FM; f16: block (idx - 2 FM) / 2, half (idx - 2 FM) % 2).
+    auto read_frag = [&](int s, int p, int idx, v4i (&xa)[FM][2], v4i (&xb)[FN][kWH]) {
+        if (idx < 2 * FM) {
             xa[idx >> 1][idx & 1] =
                 *reinterpret_cast<const v4i*>(stage(s) + offA(p, idx & 1) + (idx >> 1) * 32 * 64);
-        else
-            xb[idx - 2 * FM] = *reinterpret_cast<const v4i*>(stage(s) + offB(p) + (idx - 2 * FM) * 32 * 64);
+        } else if constexpr (WB == 8) {
+            xb[idx - 2 * FM][0] = *reinterpret_cast<const v4i*>(stage(s) + offB(p) + (idx - 2 * FM) * 32 * 64);
+        } else {
+            const int b = idx - 2 * FM;
+            xb[b >> 1][b & 1] = *reinterpret_cast<const v4i*>(stage(s) + offB16(p, b & 1) + (b >> 1) * 32 * 64);
+        }
     };
     // One pair of MFMA steps on fragments xa/xb, with one read (and one copy)
     // issued after each of the first MFMAs.
     v16f acc[FM][FN];
-    auto pair_mfmas = [&](v4i (&xa)[FM][2], v4i (&xb)[FN], auto&& after) {
+    auto pair_mfmas = [&](v4i (&xa)[FM][2], v4i (&xb)[FN][kWH], auto&& after) {
 #pragma unroll
         for (int jn = 0; jn < FN; ++jn) {
-            const u32 wd[4] = {(u32)xb[jn][0], (u32)xb[jn][1], (u32)xb[jn][2], (u32)xb[jn][3]};
-            v2h h[8];
+            v8h b0, b1;
+            if constexpr (WB == 8) {
+                const u32 wd[4] = {(u32)xb[jn][0][0], (u32)xb[jn][0][1], (u32)xb[jn][0][2], (u32)xb[jn][0][3]};
+                v2h h[8];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) i8x4_to_f16x4(wd[q], h[2 * q], h[2 * q + 1]);
-            const v8h b0 = {h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
-            const v8h b1 = {h[4][0], h[4][1], h[5][0], h[5][1], h[6][0], h[6][1], h[7][0], h[7][1]};
+                for (int q = 0; q < 4; ++q) i8x4_to_f16x4(wd[q], h[2 * q], h[2 * q + 1]);
+                b0 = v8h{h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
+                b1 = v8h{h[4][0], h[4][1], h[5][0], h[5][1], h[6][0], h[6][1], h[7][0], h[7][1]};
+            } else {
+                __builtin_memcpy(&b0, &xb[jn][0], 16);
+                __builtin_memcpy(&b1, &xb[jn][kWH - 1], 16);
+            }
 #pragma unroll
             for (int i = 0; i < FM; ++i) {
                 v8h a0, a1;
@@ -929,7 +1016,7 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     s_waitcnt_vm<0>();  // copies of clamped K tiles may still be landing
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int WB = 8>
 hipError_t launch_ring16_cfg(const W8A16Args& a, hipStream_t stream) {
     const int64_t tiles = ((a.rows + BM - 1) / BM) * ((a.columns + BN - 1) / BN);
     int dev = 0, cus = 256;
@@ -937,7 +1024,7 @@ hipError_t launch_ring16_cfg(const W8A16Args& a, hipStream_t stream) {
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         cus = 256;
     const int64_t grid = tiles < cus ? tiles : cus;
-    hipLaunchKernelGGL((w8a16_ring_kernel<BM, BN>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((w8a16_ring_kernel<BM, BN, WB>), dim3((unsigned)grid), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -960,19 +1047,13 @@ hipError_t launch_mfma16_cfg(const W8A16Args& a, hipStream_t stream) {
 hipError_t launch_w8a16_gemv(const W8A16Args& a, hipStream_t stream) {
     if (a.rows == 0 || a.columns == 0) return hipSuccess;
     switch (a.rows) {
-        case 1: return launch_gemv_m<1>(a, stream);
-        case 2: return launch_gemv_m<2>(a, stream);
-        default: return launch_gemv_m<4>(a, stream);  // 3 rows run with one zero row
+        case 1: return launch_gemv_m<1, 8>(a, stream);
+        case 2: return launch_gemv_m<2, 8>(a, stream);
+        default: return launch_gemv_m<4, 8>(a, stream);  // 3 rows run with one zero row
     }
 }
 
-hipError_t launch_w8a16_skinny(const W8A16Args& a, hipStream_t stream) {
-    if (a.rows == 0 || a.columns == 0) return hipSuccess;
-    if (a.rows <= 16) return launch_skinny_cfg<1>(a, stream);
-    if (a.rows <= 32) return launch_skinny_cfg<2>(a, stream);
-    if (a.rows <= 48) return launch_skinny_cfg<3>(a, stream);
-    return launch_skinny_cfg<4>(a, stream);
-}
+hipError_t launch_w8a16_skinny(const W8A16Args& a, hipStream_t stream) { return launch_skinny<8>(a, stream); }
 
 // OMNI_W8A16_TILE=<n> pins the prefill GEMM kernel (tuning and test aid):
 // 1 = tiled 128 x 128, 2 = tiled 64 x 64, 4/5 = ring 256 x 128 / 128 x 128
@@ -1047,6 +1128,47 @@ hipError_t launch_w4a16_mfma(const W8A16Args& a, hipStream_t stream) {
     const int64_t big_tiles = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
     if (big_tiles >= 512) return launch_mfma16_cfg<128, 128, 64, 2, 2, 4, 4>(a, stream);
     return launch_mfma16_cfg<64, 64, 64, 2, 2, 4, 4>(a, stream);
+}
+
+// ---------------------------------------------------------------------------
+// fp16 linear: the same kernels with f16 weights and no scale.
+// ---------------------------------------------------------------------------
+
+hipError_t launch_f16_gemv(const W8A16Args& a, hipStream_t stream) {
+    if (a.rows == 0 || a.columns == 0) return hipSuccess;
+    switch (a.rows) {
+        case 1: return launch_gemv_m<1, 16>(a, stream);
+        case 2: return launch_gemv_m<2, 16>(a, stream);
+        default: return launch_gemv_m<4, 16>(a, stream);
+    }
+}
+
+hipError_t launch_f16_skinny(const W8A16Args& a, hipStream_t stream) { return launch_skinny<16>(a, stream); }
+
+// OMNI_F16_TILE=<n> pins the fp16 GEMM kernel (tuning and test aid):
+// 1 = tiled 128 x 128, 2 = tiled 64 x 64, 4/5/6 = ring 256 x 128 / 128 x 128 /
+// 128 x 256 (K % 64 == 0 only). Read on every call.
+hipError_t launch_f16_mfma(const W8A16Args& a, hipStream_t stream) {
+    if (a.rows == 0 || a.columns == 0) return hipSuccess;
+    const bool ring_ok = a.width % 64 == 0;
+    const char* ov = std::getenv("OMNI_F16_TILE");
+    switch (ov ? std::atoi(ov) : 0) {
+        case 1: return launch_mfma16_cfg<128, 128, 64, 2, 2, 4, 16>(a, stream);
+        case 2: return launch_mfma16_cfg<64, 64, 64, 2, 2, 4, 16>(a, stream);
+        case 4: if (ring_ok) return launch_ring16_cfg<256, 128, 16>(a, stream); break;
+        case 5: if (ring_ok) return launch_ring16_cfg<128, 128, 16>(a, stream); break;
+        case 6: if (ring_ok) return launch_ring16_cfg<128, 256, 16>(a, stream); break;
+        default: break;
+    }
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus = 256;
+    const int64_t ring_tiles = ((a.rows + 255) / 256) * ((a.columns + 127) / 128);
+    if (ring_ok && a.width >= 3072 && ring_tiles >= cus) return launch_ring16_cfg<256, 128, 16>(a, stream);
+    const int64_t big_tiles = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
+    if (big_tiles >= 512) return launch_mfma16_cfg<128, 128, 64, 2, 2, 4, 16>(a, stream);
+    return launch_mfma16_cfg<64, 64, 64, 2, 2, 4, 16>(a, stream);
 }
 
 }  // namespace omni

@@ -8,6 +8,8 @@ path: a missing library, a non-gfx950 device or a CPU tensor raises.
 Reference interface (GoooIce/omni-rs):
   try_int8_gemm            crates/omni-kernel/src/int8_matmul.rs:505-560
   Int8Linear / hadamard    crates/qwen-image/src/convrot.rs:70-160 (see convrot.py)
+  fp16 try_linear (x2)     crates/breeze-tts/src/metal_depth.rs:84-123,
+                           crates/qwen-image/src/metal_tensorops.rs:161-203 (see f16.py)
 """
 from __future__ import annotations
 

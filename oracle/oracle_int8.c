@@ -465,3 +465,52 @@ void oracle_w4a16_gemm(const uint16_t* x, int64_t rows, int64_t width, const uin
         }
     free(w);
 }
+
+/* fp16 linear ground truth in f64, as the reference's GEMV test computes its
+ * expected value (crates/breeze-tts/src/metal_depth_tests.rs:67-73):
+ * out[m][n] = sum_k f64(x[m][k]) * f64(w[n][k]); x f16 [rows][width],
+ * w f16 [columns][width] (output-major). */
+void oracle_f16_linear_f64(const uint16_t* x, int64_t rows, int64_t width, const uint16_t* w,
+                           int64_t columns, double* out)
+{
+    double* xr = (double*)malloc((size_t)width * sizeof(double));
+    for (int64_t r = 0; r < rows; ++r) {
+        for (int64_t k = 0; k < width; ++k)
+            xr[k] = (double)oracle_f16_to_f32(x[r * width + k]);
+        for (int64_t c = 0; c < columns; ++c) {
+            const uint16_t* b = w + c * width;
+            double s = 0.0;
+            for (int64_t k = 0; k < width; ++k)
+                s += xr[k] * (double)oracle_f16_to_f32(b[k]);
+            out[r * columns + c] = s;
+        }
+    }
+    free(xr);
+}
+
+/* The reference GEMV restated (crates/breeze-tts/src/metal_depth.rs:13-35):
+ * lane l of a 32-lane group sums f32(x[k]) * f32(w[k]) over k = 32 i + l in
+ * order, in f32; the 32 partials are added (plane_sum, whose order Metal does
+ * not fix: here a butterfly over lane distances 16, 8, 4, 2, 1); the f32 sum
+ * is rounded to f16. width % 32 == 0. */
+void oracle_f16_gemv(const uint16_t* x, int64_t rows, int64_t width, const uint16_t* w,
+                     int64_t columns, uint16_t* out)
+{
+    for (int64_t r = 0; r < rows; ++r) {
+        const uint16_t* a = x + r * width;
+        for (int64_t c = 0; c < columns; ++c) {
+            const uint16_t* b = w + c * width;
+            float lane[32];
+            for (int l = 0; l < 32; ++l) {
+                float s = 0.0f;
+                for (int64_t k = l; k < width; k += 32)
+                    s += oracle_f16_to_f32(a[k]) * oracle_f16_to_f32(b[k]);
+                lane[l] = s;
+            }
+            for (int d = 16; d >= 1; d /= 2)
+                for (int l = 0; l < d; ++l)
+                    lane[l] += lane[l + d];
+            out[r * columns + c] = oracle_f32_to_f16(lane[0]);
+        }
+    }
+}

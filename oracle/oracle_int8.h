@@ -42,6 +42,12 @@
  *       quant.rs:419-462 round-trip through pack/unpack exactly; the route is
  *       within the reference test's 5e-2 (quant.rs:503) of the f64 truth and
  *       equals numpy restating dequantise -> f16 -> f32 dot on small cases.
+ *   oracle_f16_linear_f64 — numpy float64 matmul of the same halves, and the
+ *       closed form width * a * b for constant operands.
+ *   oracle_f16_gemv — within the reference test's 0.002 + 0.001 |e| of
+ *       oracle_f16_linear_f64 on its shapes and values
+ *       (metal_depth_tests.rs:16-80), and equal to numpy's f32 lane-strided
+ *       sums cast to float16.
  *   oracle_hadamard / oracle_rotate — symmetry, H*H = I within 1e-4 and the
  *       float-matmul cancellation (convrot.rs:169-220); the 4x4 base
  *       H4[a][b] = -1 iff a^b == 3 (convrot.rs:139-140); scipy.linalg.hadamard
@@ -96,6 +102,10 @@ void oracle_w4a16_f64(const uint16_t* x, int64_t rows, int64_t width, const uint
 void oracle_w4a16_gemm(const uint16_t* x, int64_t rows, int64_t width, const uint8_t* packed,
                        const uint16_t* scale_bf16, int64_t group, const uint16_t* bias,
                        int64_t columns, uint16_t* out);
+void oracle_f16_linear_f64(const uint16_t* x, int64_t rows, int64_t width, const uint16_t* w,
+                           int64_t columns, double* out);
+void oracle_f16_gemv(const uint16_t* x, int64_t rows, int64_t width, const uint16_t* w,
+                     int64_t columns, uint16_t* out);
 
 #ifdef __cplusplus
 }

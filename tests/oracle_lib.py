@@ -47,6 +47,8 @@ class Oracle:
             "oracle_w4a16_dequant": (None, [_P, _P, _I, _I, _I, ctypes.c_int, _P]),
             "oracle_w4a16_f64": (None, [_P, _I, _I, _P, _P, _I, _P, _I, _P]),
             "oracle_w4a16_gemm": (None, [_P, _I, _I, _P, _P, _I, _P, _I, _P]),
+            "oracle_f16_linear_f64": (None, [_P, _I, _I, _P, _I, _P]),
+            "oracle_f16_gemv": (None, [_P, _I, _I, _P, _I, _P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -212,4 +214,24 @@ class Oracle:
         out = np.empty((rows, columns), dtype=np.uint16)
         self.L.oracle_w4a16_gemm(_p(x16), rows, width, _p(packed), _p(scale_bf16), group, _p(bias16),
                                  columns, _p(out))
+        return out.view(np.float16)
+
+    def f16_linear_f64(self, x16, w16):
+        """x f16 [rows, width], w f16 [columns, width] -> f64 [rows, columns]."""
+        x16 = np.ascontiguousarray(x16).view(np.uint16)
+        w16 = np.ascontiguousarray(w16).view(np.uint16)
+        rows, width = x16.shape
+        columns = w16.shape[0]
+        out = np.empty((rows, columns), dtype=np.float64)
+        self.L.oracle_f16_linear_f64(_p(x16), rows, width, _p(w16), columns, _p(out))
+        return out
+
+    def f16_gemv(self, x16, w16):
+        """The reference GEMV's f32 lane-strided sums, cast to f16."""
+        x16 = np.ascontiguousarray(x16).view(np.uint16)
+        w16 = np.ascontiguousarray(w16).view(np.uint16)
+        rows, width = x16.shape
+        columns = w16.shape[0]
+        out = np.empty((rows, columns), dtype=np.uint16)
+        self.L.oracle_f16_gemv(_p(x16), rows, width, _p(w16), columns, _p(out))
         return out.view(np.float16)
