@@ -46,6 +46,8 @@ def parse():
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a 256 MiB device copy (three times): the known-size kernel "
                         "that scales rocprofv3's FETCH_SIZE / WRITE_SIZE readings")
+    p.add_argument("--configs-only", action="store_true",
+                   help="only time every BASELINE.json config (one JSON line)")
     p.add_argument("--gemm-data-sweep", action="store_true",
                    help="only time the W8A8 GEMM of both north_star shapes on random and on "
                         "constant operands (same kernels, same work): the card's power-managed "
@@ -309,10 +311,180 @@ def convrot_bench(torch, oi, gen, dev, stream, steps):
     return res
 
 
+def rotated_gemv_time(torch, gen, dev, stream, steps, M, K, N, wbytes_per_copy, make_w, run):
+    """Per-launch seconds of run(x, w) at M x K -> N over enough weight copies
+    (made by make_w) to exceed the 256 MB MALL, so every launch streams its
+    weights from HBM."""
+    copies = max(4, -(-GEMV_ROTATION_BYTES // wbytes_per_copy))
+    x = torch.randn((M, K), generator=gen, device=dev).half()
+    ws = [make_w() for _ in range(copies)]
+    idx = [0]
+
+    def one():
+        run(x, ws[idx[0] % copies])
+        idx[0] += 1
+
+    for _ in range(2 * copies):
+        one()
+    iters = copies * max(1, steps // 8)
+    g = graph_of(one, iters)
+    t = timed_graph(g, stream) / iters
+    del g, ws
+    return t, copies
+
+
+def configs_bench(torch, oi, gen, dev, stream, steps):
+    """Every BASELINE.json config on the GPU, inputs resident in HBM, HIP-event
+    timed graph replays. HBM-bound kernels report GB/s of algorithmic bytes,
+    MFMA-bound ones TOPS / TFLOP/s (2*M*N*K)."""
+    from omni_int8 import convrot
+    res = {}
+
+    def w8(N, K):
+        return lambda: torch.randint(-127, 128, (N, K), generator=gen, device=dev, dtype=torch.int8)
+
+    def s16(N):
+        return (torch.rand(N, generator=gen, device=dev) * 0.018 + 0.002).half()
+
+    # 1: weight-only GEMM M=16, K=N=4096 (the CPU-runnable case).
+    M, K, N = 16, 4096, 4096
+    sc = s16(N)
+    t, copies = rotated_gemv_time(torch, gen, dev, stream, steps, M, K, N, N * K, w8(N, K),
+                                  lambda x, w: oi.w8a16_linear(x, w, sc))
+    nb = N * K + 2 * N + 2 * M * K + 2 * M * N
+    res["1_w8a16_m16"] = {"M": M, "K": K, "N": N, "weight_copies": copies,
+                          "us": round(t * 1e6, 3), "GB/s": round(nb / t / 1e9, 1),
+                          "roofline_frac": round(nb / t / 1e9 / PEAK_HBM_GBS, 4)}
+
+    # 2: decode GEMV sweep at 7B shapes, M = 1 and 4.
+    sweep = []
+    for K, N in ((4096, 4096), (4096, 14336), (14336, 4096), (4096, 128256)):
+        sc = s16(N)
+        for M in (1, 4):
+            t, copies = rotated_gemv_time(torch, gen, dev, stream, steps, M, K, N, N * K,
+                                          w8(N, K), lambda x, w: oi.w8a16_linear(x, w, sc))
+            nb = N * K + 2 * N + 2 * M * K + 2 * M * N
+            sweep.append({"M": M, "K": K, "N": N, "weight_copies": copies,
+                          "us": round(t * 1e6, 3), "GB/s": round(nb / t / 1e9, 1),
+                          "roofline_frac": round(nb / t / 1e9 / PEAK_HBM_GBS, 4)})
+    res["2_gemv_sweep"] = sweep
+
+    def timed(fn, n=steps):
+        for _ in range(3):
+            fn()
+        g = graph_of(fn, n)
+        tt = timed_graph(g, stream) / n
+        del g
+        return tt
+
+    # 3: W8A8 prefill, M=2048, K=4096: quantise + GEMM, f16 out + f32 bias.
+    rows3 = []
+    M, K = 2048, 4096
+    x = torch.randn((M, K), generator=gen, device=dev).half()
+    for N in (4096, 14336):
+        w = w8(N, K)()
+        scale = torch.rand(N, generator=gen, device=dev) * 0.018 + 0.002
+        bias = torch.randn(N, generator=gen, device=dev)
+
+        def layer(w=w, scale=scale, bias=bias):
+            codes, rs, total = oi.quantize_rows(x)
+            oi.w8a8_gemm(codes, rs, total, w, scale, None, bias, torch.float16)
+
+        codes, rs, total = oi.quantize_rows(x)
+        t = timed(layer)
+        tg = timed(lambda w=w, scale=scale, bias=bias: oi.w8a8_gemm(
+            codes, rs, total, w, scale, None, bias, torch.float16))
+        ops = 2.0 * M * N * K
+        rows3.append({"M": M, "K": K, "N": N, "out": "f16+bias", "us": round(t * 1e6, 2),
+                      "TOPS": round(ops / t / 1e12, 1), "gemm_us": round(tg * 1e6, 2),
+                      "gemm_TOPS": round(ops / tg / 1e12, 1),
+                      "gemm_roofline_frac": round(ops / tg / 1e12 / PEAK_INT8_TOPS, 4)})
+    res["3_w8a8_prefill"] = rows3
+
+    # 4: DiT linears at M=4352 with 1% outlier channels x20, as the production
+    # Int8Linear (ConvRot rotation + quantisation, GEMM, f16 out).
+    rows4 = []
+    M = 4352
+    for name, K, N in (("qkv", 3072, 9216), ("mlp_up", 3072, 12288), ("mlp_down", 12288, 3072)):
+        x = torch.randn((M, K), generator=gen, device=dev)
+        out_ch = torch.randperm(K, generator=gen, device=dev)[: max(1, K // 100)]
+        x[:, out_ch] *= 20.0
+        x = x.half()
+        w = w8(N, K)()
+        lin = convrot.Int8Linear(K, N, w.view(torch.int32).reshape(-1),
+                                 torch.rand(N, generator=gen, device=dev) * 0.018 + 0.002,
+                                 torch.zeros(N, dtype=torch.int32, device=dev))
+        t = timed(lambda lin=lin, x=x: lin(x))
+        ops = 2.0 * M * N * K
+        rows4.append({"layer": name, "M": M, "K": K, "N": N, "out": "f16", "us": round(t * 1e6, 2),
+                      "TOPS": round(ops / t / 1e12, 1)})
+    res["4_dit_convrot_layers"] = rows4
+
+    # 5: small-VLM mix: 28 layers of (q, kv, o, gate, up, down), W8A16.
+    H, F, KV, L = 1536, 8960, 512, 28
+    dims = ((H, H), (H, KV), (H, H), (H, F), (H, F), (F, H))  # (K, N) per linear
+    layers = [[(w8(N, K)(), s16(N)) for K, N in dims] for _ in range(L)]
+    wbytes = sum(N * K + 2 * N for K, N in dims) * L
+    xp = {K: torch.randn((1024, K), generator=gen, device=dev).half() for K in (H, F)}
+    xd = {K: torch.randn((1, K), generator=gen, device=dev).half() for K in (H, F)}
+
+    def run_all(xs):
+        for lay in layers:
+            for (K, N), (w, sc) in zip(dims, lay):
+                oi.w8a16_linear(xs[K], w, sc)
+
+    t_pre = timed(lambda: run_all(xp), 3)
+    t_dec = timed(lambda: run_all(xd), 16)
+    flops = 2.0 * 1024 * sum(N * K for K, N in dims) * L
+    dbytes = wbytes + L * sum(2 * K + 2 * N for K, N in dims)
+    # The same weights with the linears that read one input concatenated
+    # along N (q with kv, gate with up), as inference engines store them:
+    # 4 launches per layer instead of 6, identical outputs.
+    fused_dims = ((H, H + KV), (H, H), (H, 2 * F), (F, H))
+    fused = [[(torch.cat([lay[0][0], lay[1][0]]), torch.cat([lay[0][1], lay[1][1]])), lay[2],
+              (torch.cat([lay[3][0], lay[4][0]]), torch.cat([lay[3][1], lay[4][1]])), lay[5]]
+             for lay in layers]
+    del layers
+
+    def run_fused(xs):
+        for lay in fused:
+            for (K, N), (w, sc) in zip(fused_dims, lay):
+                oi.w8a16_linear(xs[K], w, sc)
+
+    t_pre_f = timed(lambda: run_fused(xp), 3)
+    t_dec_f = timed(lambda: run_fused(xd), 16)
+    res["5_vlm_mix"] = {
+        "layers": L, "hidden": H, "ffn": F, "kv_out": KV, "weight_bytes": wbytes,
+        "prefill_M": 1024, "prefill_ms": round(t_pre * 1e3, 3),
+        "prefill_TFLOP/s": round(flops / t_pre / 1e12, 1),
+        "decode_step_us": round(t_dec * 1e6, 2), "decode_GB/s": round(dbytes / t_dec / 1e9, 1),
+        "decode_roofline_frac": round(dbytes / t_dec / 1e9 / PEAK_HBM_GBS, 4),
+        "total_ms_prefill_plus_128_decode": round((t_pre + 128 * t_dec) * 1e3, 2),
+        "fused_qkv_gateup": {
+            "launches_per_layer": 4, "prefill_ms": round(t_pre_f * 1e3, 3),
+            "prefill_TFLOP/s": round(flops / t_pre_f / 1e12, 1),
+            "decode_step_us": round(t_dec_f * 1e6, 2),
+            "decode_GB/s": round(dbytes / t_dec_f / 1e9, 1),
+            "decode_roofline_frac": round(dbytes / t_dec_f / 1e9 / PEAK_HBM_GBS, 4),
+            "total_ms_prefill_plus_128_decode": round((t_pre_f + 128 * t_dec_f) * 1e3, 2)}}
+    del fused
+    return res
+
+
 def main():
     args = parse()
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.configs_only:
+        import torch
+        import omni_int8 as oi
+        dev = torch.device("cuda:0")
+        torch.cuda.set_device(dev)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(0)
+        print(json.dumps({"configs": configs_bench(torch, oi, gen, dev,
+                                                   torch.cuda.current_stream(dev), args.steps)}))
         return
     if args.gemm_data_sweep:
         gemm_data_sweep(args.steps)
@@ -415,6 +587,9 @@ def main():
     # ---- ConvRot: fused rotation + quantisation, and one whole layer ---------
     convrot_res = convrot_bench(torch, oi, gen, dev, stream, args.steps)
 
+    # ---- every BASELINE.json config ----------------------------------------------
+    configs_res = configs_bench(torch, oi, gen, dev, stream, args.steps)
+
     # ---- CPU baselines (oracle, bounded samples) -----------------------------
     import oracle_lib
     oracle = oracle_lib.Oracle()
@@ -455,6 +630,7 @@ def main():
         "convrot": convrot_res,
         "w4a16_gemv": w4,
         "f16": f16_res,
+        "configs": configs_res,
     }
     print(json.dumps(line))
 

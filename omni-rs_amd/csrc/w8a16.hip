@@ -135,22 +135,27 @@ __device__ __forceinline__ int fold_index(int lane) {
 // queues full: measured on MI355X this streams within a few percent of a
 // bare read kernel of the same size, and a 525 MB weight (a 128256 x 4096
 // vocabulary head) at 7.2 TB/s.
+// B batches of R rows (R * B rows per workgroup): all R * B rows' loads are
+// issued up front, the partial sums of one batch at a time are kept and
+// folded, so each x chunk held in registers serves R * B weight rows (x is
+// read from L2 once per workgroup: 2 * MR bytes per weight byte / (R * B)).
 // WB = 16: f16 weights, no scale (the fp16 linear).
-template <int MR, int CPL, int R, int WB = 8>
+template <int MR, int CPL, int R, int WB = 8, int B = 1>
 __global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
     constexpr int V = R * MR;
+    constexpr int RB = R * B;
     static_assert((V & (V - 1)) == 0 && V <= 64, "power-of-two partial count");
     static_assert(WB == 8 || WB == 16, "int8 or f16 weights");
     constexpr int kE = WB == 8 ? 16 : 8;  // weights per 16-byte chunk
     constexpr int kP = kE / 2;            // f16 pairs of x per chunk
-    __shared__ float s_part[16][V];
+    __shared__ float s_part[16][B * V];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int T = blockDim.x;
     const int64_t K = a.width;
     const int64_t chunks = K / kE;
-    const int64_t n0 = (int64_t)blockIdx.x * R;
+    const int64_t n0 = (int64_t)blockIdx.x * RB;
 
     // x chunks: kE halves of each owned chunk and row as kP f16 pairs.
     v2h xr[CPL][MR][kP];
@@ -180,9 +185,9 @@ __global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
     // clamped, not predicated (a predicated load lets the compiler pull its
     // consumers next to it); clamped chunks meet zero activations.
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
-    v4u wv[R][CPL];
+    v4u wv[RB][CPL];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
+    for (int r = 0; r < RB; ++r) {
         const int64_t n = n0 + r < a.columns ? n0 + r : a.columns - 1;
         const uint8_t* wrow = reinterpret_cast<const uint8_t*>(a.w) + n * K * (WB / 8);
 #pragma unroll
@@ -191,8 +196,8 @@ __global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
             wv[r][j] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wrow + c * 16));
         }
     }
-    // This thread's epilogue row (tid / MR) % R: scale and bias.
-    const int64_t n_ep = min(n0 + (tid / MR) % R, a.columns - 1);
+    // This thread's epilogue row (tid / MR) % RB: scale and bias.
+    const int64_t n_ep = min(n0 + (tid / MR) % RB, a.columns - 1);
     _Float16 sc_h = (_Float16)1.0f, bi_h = (_Float16)0.0f;
     if constexpr (WB == 8) {
         sc_h = a.scale[n_ep];
@@ -201,6 +206,8 @@ __global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
         if (a.bias) bi_h = a.bias[n_ep];
     }
 
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
     float part[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) part[i] = 0.0f;
@@ -208,7 +215,8 @@ __global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
     for (int r = 0; r < R; ++r) {
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-            const u32 words[4] = {wv[r][j].x, wv[r][j].y, wv[r][j].z, wv[r][j].w};
+            const v4u wq = wv[b * R + r][j];
+            const u32 words[4] = {wq.x, wq.y, wq.z, wq.w};
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 if constexpr (WB == 8) {
@@ -231,9 +239,10 @@ __global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
         }
     }
     Fold<V, 32>::run(part, lane);
-    if ((lane & (64 / V - 1)) == 0) s_part[wave][fold_index<V>(lane)] = part[0];
+    if ((lane & (64 / V - 1)) == 0) s_part[wave][b * V + fold_index<V>(lane)] = part[0];
+    }
     __syncthreads();
-    if (tid < V) {
+    if (tid < B * V) {
         const int r = tid / MR, m = tid % MR;
         const int64_t n = n0 + r;
         if (n < a.columns && m < a.rows) {
@@ -254,14 +263,14 @@ int gemv_cfg_override(int wb) {
     return v ? std::atoi(v) : 0;
 }
 
-template <int MR, int CPL, int R, int WB>
+template <int MR, int CPL, int R, int WB, int B = 1>
 hipError_t launch_gemv_cfg(const W8A16Args& a, hipStream_t stream) {
     const int64_t chunks = a.width / (WB == 8 ? 16 : 8);
     const int64_t lanes = (chunks + CPL - 1) / CPL;
     const int64_t T = ((lanes + 63) / 64) * 64;
     if (T > 1024) return hipErrorInvalidValue;  // the caller bounds width
-    const int64_t grid = (a.columns + R - 1) / R;
-    hipLaunchKernelGGL((w8a16_gemv_kernel<MR, CPL, R, WB>), dim3((unsigned)grid), dim3((unsigned)T), 0,
+    const int64_t grid = (a.columns + R * B - 1) / (R * B);
+    hipLaunchKernelGGL((w8a16_gemv_kernel<MR, CPL, R, WB, B>), dim3((unsigned)grid), dim3((unsigned)T), 0,
                        stream, a);
     return hipGetLastError();
 }
@@ -277,6 +286,12 @@ hipError_t launch_gemv_m(const W8A16Args& a, hipStream_t stream) {
         case 22: return launch_gemv_cfg<MR, 2, 2, WB>(a, stream);
         case 24: return launch_gemv_cfg<MR, 2, 4, WB>(a, stream);
         case 41: return launch_gemv_cfg<MR, 4, 1, WB>(a, stream);
+        case 142: return launch_gemv_cfg<MR, 1, 4, WB, 2>(a, stream);
+        case 144: return launch_gemv_cfg<MR, 1, 4, WB, 4>(a, stream);
+        case 124: return launch_gemv_cfg<MR, 1, 2, WB, 4>(a, stream);
+        case 182: return launch_gemv_cfg<MR, 1, 8, WB, 2>(a, stream);
+        case 242: return launch_gemv_cfg<MR, 2, 4, WB, 2>(a, stream);
+        case 222: return launch_gemv_cfg<MR, 2, 2, WB, 2>(a, stream);
         default: break;
     }
     const int64_t chunks = a.width / (WB == 8 ? 16 : 8);
@@ -290,12 +305,14 @@ hipError_t launch_gemv_m(const W8A16Args& a, hipStream_t stream) {
         return launch_gemv_cfg<MR, 1, 4, WB>(a, stream);
     }
     // Measured on MI355X over the BASELINE decode shapes: 64 bytes of weights
-    // in flight per lane (128 with four activation rows), two chunks per
-    // lane once a row is wider than 512 chunks, and more, smaller
-    // workgroups when the whole matrix is a few MB.
+    // in flight per lane, two chunks per lane once a row is wider than 512
+    // chunks, and more, smaller workgroups when the whole matrix is a few MB.
+    // Four activation rows: 16 rows per workgroup in two batches of 8 (x is
+    // then re-read from L2 for one eighth of the weight bytes, not a half),
+    // 10-15 % faster than 8 rows on the 14336- and 128256-row shapes.
     if (a.columns * a.width <= (4 << 20)) return launch_gemv_cfg<MR, 2, 1, WB>(a, stream);
+    if (MR == 4 && chunks <= 1024) return launch_gemv_cfg<MR, 1, 8, WB, 2>(a, stream);
     if (chunks > 512) return launch_gemv_cfg<MR, 2, 4, WB>(a, stream);
-    if (MR == 4) return launch_gemv_cfg<MR, 1, 8, WB>(a, stream);
     return launch_gemv_cfg<MR, 1, 4, WB>(a, stream);
 }
 
@@ -337,11 +354,14 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_kernel(W8A16Args a) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[mb] = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
     const int64_t steps = (K + 63) / 64;
-    auto step = [&](int64_t st) {
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    // P steps per trip, all their loads issued before any MFMA (a wave's
+    // steps are 16 apart, so a trip covers 16 P consecutive steps of the
+    // workgroup): at K = 4096 every load of the workgroup is in flight at
+    // once. Steps past K load nothing and meet zeros.
+    constexpr int P = MB <= 2 ? 4 : 2;
+    auto load = [&](int64_t st, v4u (&wv)[WB / 8], uint4 (&xv)[MB][2]) {
         const int64_t k = st * 64 + 16 * g;
-        typedef unsigned v4u __attribute__((ext_vector_type(4)));
-        v4u wv[WB / 8];
-        uint4 xv[MB][2];
         // K % 16 == 0: a lane's 16-element block is wholly inside or outside.
         if (k < K) {
 #pragma unroll
@@ -358,6 +378,8 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_kernel(W8A16Args a) {
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) xv[mb][0] = xv[mb][1] = make_uint4(0, 0, 0, 0);
         }
+    };
+    auto compute = [&](const v4u (&wv)[WB / 8], const uint4 (&xv)[MB][2]) {
         v8h b0, b1;
         if constexpr (WB == 8) {
             v2h h[8];
@@ -380,12 +402,14 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_kernel(W8A16Args a) {
             acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b1, acc[mb], 0, 0, 0);
         }
     };
-    int64_t st = wave;
-    for (; st + 16 < steps; st += 32) {  // two steps per trip: their loads overlap
-        step(st);
-        step(st + 16);
+    for (int64_t st = wave; st < steps; st += 16 * P) {
+        v4u wv[P][WB / 8];
+        uint4 xv[P][MB][2];
+#pragma unroll
+        for (int p = 0; p < P; ++p) load(st + 16 * p, wv[p], xv[p]);
+#pragma unroll
+        for (int p = 0; p < P; ++p) compute(wv[p], xv[p]);
     }
-    if (st < steps) step(st);
     // 16 x 16 accumulator layout: lane holds column lane % 16, rows
     // 4 (lane / 16) .. +3.
 #pragma unroll
@@ -781,7 +805,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a16_mfma_kernel(W
 // of the pair are summed once. Codes become f16 exactly in registers (v_perm
 // and one subtract, as in the GEMV). The schedule is the W8A8 ring's: one
 // fragment read and one copy behind each MFMA, one barrier per K tile between
-// the two pairs, the next tile's first copies issued before the epilogue.
+// the two pairs, the next tile's first copies issued before the epilogue. A
+// stage is refilled as soon as the barrier after its last fragment reads has
+// passed (tile kt+S into stage kt % S), so two tiles are in flight.
 //
 // WB = 16 (the fp16 linear): W is f16 and staged like x, as two [BN][64-byte]
 // halves, and its fragments are read like x's (two ds_read_b128 per pair);
@@ -895,34 +921,39 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
         }
     };
     // One pair of MFMA steps on fragments xa/xb, with one read (and one copy)
-    // issued after each of the first MFMAs.
+    // issued after each of the first MFMAs. The W codes of every column block
+    // are converted first; then the k 0..7 products of all FM x FN blocks run,
+    // then the k 8..15 ones, so no MFMA waits for the one just before it (two
+    // back-to-back MFMAs into one accumulator would serialise).
     v16f acc[FM][FN];
     auto pair_mfmas = [&](v4i (&xa)[FM][2], v4i (&xb)[FN][kWH], auto&& after) {
+        v8h bh[FN][2];
 #pragma unroll
         for (int jn = 0; jn < FN; ++jn) {
-            v8h b0, b1;
             if constexpr (WB == 8) {
                 const u32 wd[4] = {(u32)xb[jn][0][0], (u32)xb[jn][0][1], (u32)xb[jn][0][2], (u32)xb[jn][0][3]};
                 v2h h[8];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) i8x4_to_f16x4(wd[q], h[2 * q], h[2 * q + 1]);
-                b0 = v8h{h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
-                b1 = v8h{h[4][0], h[4][1], h[5][0], h[5][1], h[6][0], h[6][1], h[7][0], h[7][1]};
+                bh[jn][0] = v8h{h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
+                bh[jn][1] = v8h{h[4][0], h[4][1], h[5][0], h[5][1], h[6][0], h[6][1], h[7][0], h[7][1]};
             } else {
-                __builtin_memcpy(&b0, &xb[jn][0], 16);
-                __builtin_memcpy(&b1, &xb[jn][kWH - 1], 16);
+                __builtin_memcpy(&bh[jn][0], &xb[jn][0], 16);
+                __builtin_memcpy(&bh[jn][1], &xb[jn][kWH - 1], 16);
             }
+        }
 #pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                v8h a0, a1;
-                __builtin_memcpy(&a0, &xa[i][0], 16);
-                __builtin_memcpy(&a1, &xa[i][1], 16);
-                acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, acc[i][jn], 0, 0, 0);
-                after(2 * (jn * FM + i));
-                __builtin_amdgcn_sched_barrier(0);
-                acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b1, acc[i][jn], 0, 0, 0);
-                after(2 * (jn * FM + i) + 1);
-                __builtin_amdgcn_sched_barrier(0);
+        for (int half = 0; half < 2; ++half) {
+#pragma unroll
+            for (int jn = 0; jn < FN; ++jn) {
+#pragma unroll
+                for (int i = 0; i < FM; ++i) {
+                    v8h av;
+                    __builtin_memcpy(&av, &xa[i][half], 16);
+                    acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bh[jn][half], acc[i][jn], 0, 0, 0);
+                    after(half * FM * FN + jn * FM + i);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
         }
     };
@@ -934,7 +965,7 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     load_params(n0);
     store_params(0);
 #pragma unroll
-    for (int u = 0; u < S - 1; ++u) copy_tile(u, u);
+    for (int u = 0; u < S; ++u) copy_tile(u, u);
     int parity = 0;
 
     while (true) {
@@ -950,7 +981,7 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
 #pragma unroll
             for (int j = 0; j < FN; ++j) acc[i][j] = v16f{};
 
-        s_waitcnt_vm<(S - 2) * kCpw, true>();
+        s_waitcnt_vm<(S - 1) * kCpw, true>();
         lds_barrier();
 #pragma unroll
         for (int idx = 0; idx < kFrags; ++idx) read_frag(0, 0, idx, xa0, xb0);
@@ -964,11 +995,11 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
                     pair_mfmas(xa0, xb0, [&](int q) {
                         if (q < kFrags) read_frag(u, 1, q, xa1, xb1);
                     });
-                    s_waitcnt_vm<(S - 3) * kCpw, true>();
-                    lds_barrier();  // tile kt+1 landed everywhere; stage (u+S-1)%S is free
-                    // Pair 1 of tile kt; copies of tile kt+S-1; reads of tile kt+1, pair 0.
+                    s_waitcnt_vm<(S - 2) * kCpw, true>();
+                    lds_barrier();  // tile kt+1 landed everywhere; stage u is read
+                    // Pair 1 of tile kt; copies of tile kt+S into stage u; reads of tile kt+1, pair 0.
                     pair_mfmas(xa1, xb1, [&](int q) {
-                        if (q < kCpw) copy_one(kt + S - 1, (u + S - 1) % S, q);
+                        if (q < kCpw) copy_one(kt + S, u, q);
                         if (q < kFrags) read_frag((u + 1) % S, 0, q, xa0, xb0);
                     });
                 }
@@ -976,7 +1007,7 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
         }
 
         const int64_t em0 = m0, en0 = n0;
-        s_waitcnt_vm<(S - 2) * kCpw, true>();
+        s_waitcnt_vm<(S - 1) * kCpw, true>();
         lds_barrier();  // every wave is done reading the ring
         if (more) {
             m0 = nm0;
@@ -984,7 +1015,7 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
             setup_copies();
             store_params(parity ^ 1);
 #pragma unroll
-            for (int u = 0; u < S - 1; ++u) copy_tile(u, u);
+            for (int u = 0; u < S; ++u) copy_tile(u, u);
         }
 
         // Epilogue: out = f16(acc * scale[n] + bias[n]). 32x32 accumulator
@@ -1071,6 +1102,7 @@ hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream) {
         case 2: return launch_mfma16_cfg<64, 64, 64, 2, 2, 4>(a, stream);
         case 4: if (ring_ok) return launch_ring16_cfg<256, 128>(a, stream); break;
         case 5: if (ring_ok) return launch_ring16_cfg<128, 128>(a, stream); break;
+        case 6: if (ring_ok) return launch_ring16_cfg<256, 256>(a, stream); break;
         default: break;
     }
     // Measured on MI355X (config 5 and the BASELINE GEMM shapes): the ring

@@ -568,13 +568,15 @@ __global__ __launch_bounds__(128 * WAVES_M, 512 / (128 * WAVES_M)) void w8a8_dma
 // Persistent LDS-DMA ring GEMM (K % 64 == 0, S divides the K-tile count).
 // One workgroup of 4 waves per CU walks 256 x BN output tiles; each wave owns
 // a 128 x BN/2 block of 32x32 int32 accumulators (AGPRs). K tiles of 64 bytes
-// reach LDS through global_load_lds_dwordx4 into an S-stage ring (S-1 tiles
-// in flight, distinct LDS arrays so each copy and read names its stage
-// statically). Per K tile the schedule is
+// reach LDS through global_load_lds_dwordx4 into an S-stage ring (distinct
+// LDS arrays so each copy and read names its stage statically). Per K tile
+// the schedule is
 //   MFMAs (tile kt, k step 0)    | fragment reads (tile kt, k step 1)
-//   wait for tile kt+1's copies, barrier
-//   MFMAs (tile kt, k step 1)    | copy tile kt+S-1 into the freed stage,
+//   wait for tile kt+1's copies, barrier (stage kt % S is now fully read)
+//   MFMAs (tile kt, k step 1)    | copy tile kt+S into stage kt % S,
 //                                | fragment reads (tile kt+1, k step 0)
+// so S-1 tiles are in flight across the barrier: a copy is issued about S-1
+// K tiles before its data is read.
 // with one read and one copy issued after each MFMA, so every LDS read has
 // most of an MFMA group to land, no copy burst holds up an MFMA, and the only
 // barrier sits between two MFMA groups. (With one wave per SIMD a copy that
@@ -717,7 +719,7 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
     load_params(m0, n0);
     store_params(0);
 #pragma unroll
-    for (int u = 0; u < S - 1; ++u) copy_tile(u, u);
+    for (int u = 0; u < S; ++u) copy_tile(u, u);
     int parity = 0;
 
     while (true) {
@@ -736,7 +738,7 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
             for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
 
         // Tile 0's copies (and the parameter stores) visible to every wave.
-        s_waitcnt_vm<(S - 2) * kCpw, true>();
+        s_waitcnt_vm<(S - 1) * kCpw, true>();
         lds_barrier();
         read_frags(0, 0, fa0, fb0);
 
@@ -756,15 +758,15 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
                     if (q < FM + FN) read_frag(u, 1, q, fa1, fb1);
                     __builtin_amdgcn_sched_barrier(0);
                 }
-                s_waitcnt_vm<(S - 3) * kCpw, true>();
-                lds_barrier();  // tile kt+1 landed everywhere; stage (u+S-1)%S is free
-                // k step 1: after each MFMA, one copy of tile kt+S-1 into the
-                // freed stage and one fragment read of tile kt+1, k step 0.
+                s_waitcnt_vm<(S - 2) * kCpw, true>();
+                lds_barrier();  // tile kt+1 landed everywhere; stage u is read
+                // k step 1: after each MFMA, one copy of tile kt+S into stage
+                // u and one fragment read of tile kt+1, k step 0.
 #pragma unroll
                 for (int q = 0; q < FM * FN; ++q) {
                     const int i = q / FN, j = q % FN;
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1[i], fb1[j], acc[i][j], 0, 0, 0);
-                    if (q < kCpw) copy_one(kt + S - 1, (u + S - 1) % S, q);
+                    if (q < kCpw) copy_one(kt + S, u, q);
                     if (q < FM + FN) read_frag((u + 1) % S, 0, q, fa0, fb0);
                     __builtin_amdgcn_sched_barrier(0);
                 }
@@ -772,8 +774,10 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
         }
 
         const int64_t em0 = m0, en0 = n0;
-        // Every wave is done reading the ring before the next tile's copies.
-        s_waitcnt_vm<(S - 2) * kCpw, true>();
+        // Every wave is done reading the ring before the next tile's copies
+        // (the clamped copies still in flight land first: one wave's loads
+        // complete in issue order, and each wave writes its own LDS chunks).
+        s_waitcnt_vm<(S - 1) * kCpw, true>();
         lds_barrier();
         if (more) {
             m0 = nm0;
@@ -781,7 +785,7 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
             setup_copies();
             store_params(parity ^ 1);
 #pragma unroll
-            for (int u = 0; u < S - 1; ++u) copy_tile(u, u);
+            for (int u = 0; u < S; ++u) copy_tile(u, u);
         }
 
         // Epilogue. 32x32 accumulator layout: lane holds column (lane & 31)

@@ -64,11 +64,14 @@ def test_gemv_small_and_odd_shapes(oracle, rows, width, columns):
     assert tolerance.rel_err(got, route.astype(np.float64)) <= tolerance.FP16_REL_TOL
 
 
-@pytest.mark.parametrize("cfg", ["11", "12", "14", "18", "21", "22", "24"])
+@pytest.mark.parametrize("cfg", ["11", "12", "14", "18", "21", "22", "24",
+                                 "142", "144", "124", "182", "242", "222"])
 def test_gemv_every_configuration(oracle, monkeypatch, cfg):
     # OMNI_W8A16_GEMV pins one GEMV instantiation (chunks per lane, rows per
-    # workgroup); each must agree with the oracle on ragged shapes, including
-    # the widest row (16384) and a row narrower than one wavefront of chunks.
+    # batch, and batches per workgroup when there are three digits); each must
+    # agree with the oracle on ragged shapes, including the widest row (16384),
+    # a row narrower than one wavefront of chunks and column counts that leave
+    # the last workgroup's batches partly or wholly past the matrix.
     monkeypatch.setenv("OMNI_W8A16_GEMV", cfg)
     for rows, width, columns in ((1, 4096, 77), (4, 16384, 9), (3, 1536, 130), (2, 16, 5),
                                  (1, 14336, 31)):
@@ -141,12 +144,12 @@ def test_skinny_rows_on_both_routes(oracle, monkeypatch, route, rows, width, col
     assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL, (route, rows, width, columns)
 
 
-@pytest.mark.parametrize("tile", ["1", "2", "4", "5"])
+@pytest.mark.parametrize("tile", ["1", "2", "4", "5", "6"])
 @pytest.mark.parametrize("rows,width,columns", [(300, 512, 200), (1024, 1536, 1536), (257, 8960, 129),
-                                                (197, 4096, 640), (65, 64, 33)])
+                                                (197, 4096, 640), (65, 64, 33), (600, 4096, 700)])
 def test_every_prefill_kernel(oracle, monkeypatch, tile, rows, width, columns):
     # OMNI_W8A16_TILE pins one prefill kernel: the tiled GEMMs (1, 2) and the
-    # LDS-DMA ring GEMMs (4 = 256 x 128, 5 = 128 x 128); ragged rows/columns,
+    # LDS-DMA ring GEMMs (4 = 256 x 128, 5 = 128 x 128, 6 = 256 x 256); ragged rows/columns,
     # bias, against the f64 ground truth
     monkeypatch.setenv("OMNI_W8A16_TILE", tile)
     rng = np.random.default_rng(rows + width + columns + int(tile))
