@@ -121,6 +121,37 @@ __device__ __forceinline__ void lds_copy16(const uint8_t* src, uint8_t* lds_dst)
 #endif
 }
 
+// The same copy as inline assembly: the compiler then sees no LDS write in
+// flight, so it inserts no vmcnt wait of its own before a later LDS read
+// (where it cannot tell which ring stage a copy targets it waits for every
+// outstanding operation, a full pipeline drain per K tile). The caller's
+// explicit waits order the copies. lds_dst must be wave-uniform.
+// The same, addressed as a wave-uniform 64-bit base (SGPRs) plus a 32-bit
+// per-lane byte offset (no per-lane 64-bit pointer is held or added), and
+// with the LDS byte address given as a wave-uniform integer (see lds_addr).
+__device__ __forceinline__ void lds_copy16_saddr(unsigned voff, const void* base, unsigned lds_byte) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds_byte)
+                 : "memory", "m0");
+#endif
+}
+
+// LDS byte address of a __shared__ object, as a wave-uniform integer.
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const OMNI_LDS void*)p);
+#else
+    (void)p;
+    return 0;
+#endif
+}
+__device__ __forceinline__ void lds_copy16_asm(const void* src, void* lds_dst) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(OMNI_LDS void*)lds_dst);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+#endif
+}
+
 
 // s_waitcnt vmcnt(N) (and lgkmcnt(0) when LGKM0) for a compile-time N.
 template <int N, bool LGKM0 = false>

@@ -812,10 +812,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a16_mfma_kernel(W
 // WB = 16 (the fp16 linear): W is f16 and staged like x, as two [BN][64-byte]
 // halves, and its fragments are read like x's (two ds_read_b128 per pair);
 // there is no scale.
-template <int BM, int BN, int WB = 8>
+template <int BM, int BN, int WB = 8, int WMW = 2>
 __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     constexpr int S = 3;
-    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int WNW = 4 / WMW;              // waves along N
+    constexpr int WM = BM / WMW, WN = BN / WNW;
     constexpr int FM = WM / 32, FN = WN / 32;
     constexpr int kWH = WB / 8;               // 64-byte W rows per column per K tile
     constexpr int kRows = 2 * BM + kWH * BN;  // 64-byte stage rows: x k 0..31, x k 32..63, W
@@ -834,7 +835,7 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WNW, wn = wave % WNW;
     const int tiles_m = (int)((a.rows + BM - 1) / BM);
     const int tiles_n = (int)((a.columns + BN - 1) / BN);
     const int total = tiles_m * tiles_n;
@@ -843,13 +844,13 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     const bool has_bias = a.bias != nullptr;
     constexpr int kGroupM = 4;
     auto stage = [&](int s) -> uint8_t* { return s == 0 ? st0 : s == 1 ? st1 : st2; };
+    const unsigned stage_lds[3] = {lds_addr(st0), lds_addr(st1), lds_addr(st2)};
 
     // Copy c fills stage rows 16c .. 16c+15; lane l reads logical chunk
     // (l % 4) ^ ((l / 16) % 4) of row l / 4, landing at physical chunk l % 4.
     const int cp_row = lane >> 2;
     const int cp_chunk = (lane & 3) ^ ((lane >> 4) & 3);
-    const uint8_t* src[kCpw];
-    int adv[kCpw];  // bytes per K tile: 128 for x and f16 W rows (64 halves), 64 for int8 W rows
+    unsigned voff[kCpw];
     int64_t m0 = 0, n0 = 0;
     float p_sc = 0.0f, p_bi = 0.0f;
     auto tile_origin = [&](int l, int64_t& tm0, int64_t& tn0) {
@@ -859,6 +860,9 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
         tm0 = (int64_t)__builtin_amdgcn_readfirstlane(first_m + (l % group_size) % gm) * BM;
         tn0 = (int64_t)__builtin_amdgcn_readfirstlane((l % group_size) / gm) * BN;
     };
+    // Copy j reads one matrix (x or W, wave-uniform) at a per-lane 32-bit byte
+    // offset from its base (the host keeps both matrices under 4 GiB); the K
+    // tile advance is added to the scalar base.
     auto setup_copies = [&]() {
 #pragma unroll
         for (int j = 0; j < kCpw; ++j) {
@@ -866,14 +870,12 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
             if (c16 < 2 * BM) {
                 const int half = c16 >= BM;
                 const int64_t row = min(m0 + (c16 - half * BM) + cp_row, a.rows - 1);
-                src[j] = reinterpret_cast<const uint8_t*>(a.x + row * K) + half * 64 + cp_chunk * 16;
-                adv[j] = 128;
+                voff[j] = (unsigned)(row * K * 2) + half * 64 + cp_chunk * 16;
             } else {
                 const int rel = c16 - 2 * BM;
                 const int half = WB == 16 && rel >= BN;
                 const int64_t row = min(n0 + (rel - half * BN) + cp_row, a.columns - 1);
-                src[j] = reinterpret_cast<const uint8_t*>(a.w) + row * K * kWH + half * 64 + cp_chunk * 16;
-                adv[j] = 64 * kWH;
+                voff[j] = (unsigned)(row * K * kWH) + half * 64 + cp_chunk * 16;
             }
         }
     };
@@ -892,7 +894,10 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     };
     auto copy_one = [&](int kt, int s, int j) {
         const int64_t kk = min(kt, ktiles - 1);
-        lds_copy16(src[j] + kk * adv[j], stage(s) + wave * kCpw * 1024 + j * 1024);
+        const bool is_x = (wave * kCpw + j) * 16 < 2 * BM;  // wave-uniform
+        const uint8_t* base = is_x ? reinterpret_cast<const uint8_t*>(a.x) + kk * 128
+                                   : reinterpret_cast<const uint8_t*>(a.w) + kk * 64 * kWH;
+        lds_copy16_saddr(voff[j], base, stage_lds[s] + (wave * kCpw + j) * 1024);
     };
     auto copy_tile = [&](int kt, int s) {
 #pragma unroll
@@ -1020,24 +1025,35 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
 
         // Epilogue: out = f16(acc * scale[n] + bias[n]). 32x32 accumulator
         // layout: lane holds column lane % 32, rows 8 (r / 4) + 4 (lane / 32) + r % 4.
+        // Offsets are 32-bit from the tile's first element (the host keeps
+        // 256 * columns below 2^31); the lane indices pass through an empty
+        // asm so the compiler does not precompute every store address.
         const float* pScale = sScale[parity];
         const float* pBias = sBias[parity];
+        {
+            const int N = (int)a.columns;
+            _Float16* outt = a.out + em0 * a.columns + en0;
+            const int rows_last = (int)min((int64_t)BM, a.rows - em0) - 1;
+            const int cols_last = (int)min((int64_t)BN, a.columns - en0) - 1;
+            int efr = fr, efh = fh;
+            asm volatile("" : "+v"(efr), "+v"(efh));
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
+            for (int i = 0; i < FM; ++i) {
 #pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                const int lc = wn * WN + j * 32 + fr;
-                const int64_t col = en0 + lc;
-                const float sc = pScale[lc];
-                const float bi = pBias[lc];
+                for (int j = 0; j < FN; ++j) {
+                    const int lc = wn * WN + j * 32 + efr;
+                    const float sc = pScale[lc];
+                    const float bi = pBias[lc];
+                    const int lr0 = wm * WM + i * 32 + 4 * efh;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int64_t row = em0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * fh + (r & 3);
-                    if (row < a.rows && col < a.columns)
-                        __builtin_nontemporal_store((_Float16)(acc[i][j][r] * sc + bi),
-                                                    a.out + row * a.columns + col);
+                    for (int r = 0; r < 16; ++r) {
+                        const int lr = lr0 + 8 * (r >> 2) + (r & 3);
+                        if (lc <= cols_last && lr <= rows_last)
+                            __builtin_nontemporal_store((_Float16)(acc[i][j][r] * sc + bi),
+                                                        outt + (unsigned)(lr * N + lc));
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
                 }
-                __builtin_amdgcn_sched_barrier(0);
             }
         }
         if (!more) break;
@@ -1047,7 +1063,15 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     s_waitcnt_vm<0>();  // copies of clamped K tiles may still be landing
 }
 
-template <int BM, int BN, int WB = 8>
+// The ring kernel's limits: 64-element K tiles, per-lane copy offsets of x
+// and W rows in 32 bits, in-tile output offsets in 32 bits.
+bool ring16_fits(const W8A16Args& a) {
+    const int64_t lim = int64_t(1) << 32;
+    return a.width % 64 == 0 && a.rows * a.width * 2 < lim && a.columns * a.width * 2 < lim &&
+           a.columns < (int64_t(1) << 23);
+}
+
+template <int BM, int BN, int WB = 8, int WMW = 2>
 hipError_t launch_ring16_cfg(const W8A16Args& a, hipStream_t stream) {
     const int64_t tiles = ((a.rows + BM - 1) / BM) * ((a.columns + BN - 1) / BN);
     int dev = 0, cus = 256;
@@ -1055,7 +1079,7 @@ hipError_t launch_ring16_cfg(const W8A16Args& a, hipStream_t stream) {
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         cus = 256;
     const int64_t grid = tiles < cus ? tiles : cus;
-    hipLaunchKernelGGL((w8a16_ring_kernel<BM, BN, WB>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((w8a16_ring_kernel<BM, BN, WB, WMW>), dim3((unsigned)grid), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -1087,8 +1111,9 @@ hipError_t launch_w8a16_gemv(const W8A16Args& a, hipStream_t stream) {
 hipError_t launch_w8a16_skinny(const W8A16Args& a, hipStream_t stream) { return launch_skinny<8>(a, stream); }
 
 // OMNI_W8A16_TILE=<n> pins the prefill GEMM kernel (tuning and test aid):
-// 1 = tiled 128 x 128, 2 = tiled 64 x 64, 4/5 = ring 256 x 128 / 128 x 128
-// (K % 64 == 0 only). Read on every call.
+// 1 = tiled 128 x 128, 2 = tiled 64 x 64, 4/5/6 = ring 256 x 128 / 128 x 128 /
+// 256 x 256 (2 x 2 waves), 7 = ring 256 x 256 (1 x 4 waves) (rings: K % 64
+// == 0 only). Read on every call.
 int w8a16_tile_override() {
     const char* v = std::getenv("OMNI_W8A16_TILE");
     return v ? std::atoi(v) : 0;
@@ -1096,13 +1121,14 @@ int w8a16_tile_override() {
 
 hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream) {
     if (a.rows == 0 || a.columns == 0) return hipSuccess;
-    const bool ring_ok = a.width % 64 == 0;
+    const bool ring_ok = ring16_fits(a);
     switch (w8a16_tile_override()) {
         case 1: return launch_mfma16_cfg<128, 128, 64, 2, 2, 4>(a, stream);
         case 2: return launch_mfma16_cfg<64, 64, 64, 2, 2, 4>(a, stream);
         case 4: if (ring_ok) return launch_ring16_cfg<256, 128>(a, stream); break;
         case 5: if (ring_ok) return launch_ring16_cfg<128, 128>(a, stream); break;
         case 6: if (ring_ok) return launch_ring16_cfg<256, 256>(a, stream); break;
+        case 7: if (ring_ok) return launch_ring16_cfg<256, 256, 8, 1>(a, stream); break;
         default: break;
     }
     // Measured on MI355X (config 5 and the BASELINE GEMM shapes): the ring
@@ -1112,8 +1138,17 @@ hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream) {
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         cus = 256;
+    // 256 x 256 tiles with the four waves side by side along N (each wave
+    // 256 x 64: every weight code is converted by one wave only) once they
+    // fill a round of CUs: 1030-1140 TFLOP/s at 4096 x 4096 x 12288..14336,
+    // against 970 for 256 x 128 tiles.
+    const int64_t wide_tiles = ((a.rows + 255) / 256) * ((a.columns + 255) / 256);
+    if (ring_ok && a.width >= 3072 && wide_tiles >= cus) return launch_ring16_cfg<256, 256, 8, 1>(a, stream);
     const int64_t ring_tiles = ((a.rows + 255) / 256) * ((a.columns + 127) / 128);
     if (ring_ok && a.width >= 3072 && ring_tiles >= cus) return launch_ring16_cfg<256, 128>(a, stream);
+    // Smaller prefill shapes (config 5's M = 1024 linears, K 1536 and 8960):
+    // the 128 x 128 ring beats the register-staged tiled kernels by 10-35 %.
+    if (ring_ok) return launch_ring16_cfg<128, 128>(a, stream);
     const int64_t big_tiles = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
     if (big_tiles >= 512) return launch_mfma16_cfg<128, 128, 64, 2, 2, 4>(a, stream);
     return launch_mfma16_cfg<64, 64, 64, 2, 2, 4>(a, stream);
@@ -1182,7 +1217,7 @@ hipError_t launch_f16_skinny(const W8A16Args& a, hipStream_t stream) { return la
 // 128 x 256 (K % 64 == 0 only). Read on every call.
 hipError_t launch_f16_mfma(const W8A16Args& a, hipStream_t stream) {
     if (a.rows == 0 || a.columns == 0) return hipSuccess;
-    const bool ring_ok = a.width % 64 == 0;
+    const bool ring_ok = ring16_fits(a);
     const char* ov = std::getenv("OMNI_F16_TILE");
     switch (ov ? std::atoi(ov) : 0) {
         case 1: return launch_mfma16_cfg<128, 128, 64, 2, 2, 4, 16>(a, stream);
