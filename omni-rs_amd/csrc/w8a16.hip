@@ -456,18 +456,19 @@ hipError_t launch_skinny(const W8A16Args& a, hipStream_t stream) {
 // scale group (group % 32 == 0), so the chunk's dot is taken on the exact
 // codes and multiplied by its scale once. A workgroup of T = 64 * ceil(K /
 // 2048) lanes owns R weight rows; every weight load is issued up front.
-template <int MR, int R>
+template <int MR, int R, int B = 1>
 __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W8A16Args a) {
     constexpr int V = R * MR;
+    constexpr int RB = R * B;  // rows per workgroup: B batches of R
     static_assert((V & (V - 1)) == 0 && V <= 64, "power-of-two partial count");
-    __shared__ float s_part[16][V];
+    __shared__ float s_part[16][B * V];
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int T = blockDim.x;
     const int64_t K = a.width;
     const int64_t chunks = K / 32;
     const int64_t gpr = K / a.group;  // scale groups per weight row
-    const int64_t n0 = (int64_t)blockIdx.x * R;
+    const int64_t n0 = (int64_t)blockIdx.x * RB;
     const bool live = tid < chunks;
     const int64_t c = live ? tid : chunks - 1;  // clamped: meets zero activations
 
@@ -490,28 +491,31 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W8A16Args a) {
             for (int e = 0; e < 16; ++e) xr[m][e] = v2h{};
         }
     }
-    v4u wv[R];
-    float sc[R];
+    v4u wv[RB];
+    float sc[RB];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
+    for (int r = 0; r < RB; ++r) {
         const int64_t n = n0 + r < a.columns ? n0 + r : a.columns - 1;
         wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(a.w + n * (K / 2) + c * 16));
     }
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
+    for (int r = 0; r < RB; ++r) {
         const int64_t n = n0 + r < a.columns ? n0 + r : a.columns - 1;
         sc[r] = bf16_to_f32(a.gscale[n * gpr + (c * 32) / a.group]);
     }
-    const int64_t n_ep = min(n0 + (tid / MR) % R, a.columns - 1);
+    const int64_t n_ep = min(n0 + (tid / MR) % RB, a.columns - 1);
     const _Float16 bi_h = a.bias ? a.bias[n_ep] : (_Float16)0.0f;
 
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
     float part[V];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         float d[MR];
 #pragma unroll
         for (int m = 0; m < MR; ++m) d[m] = 0.0f;
-        const u32 words[4] = {wv[r].x, wv[r].y, wv[r].z, wv[r].w};
+        const v4u wq = wv[b * R + r];
+        const u32 words[4] = {wq.x, wq.y, wq.z, wq.w};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             v2h h[4];
@@ -522,12 +526,13 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W8A16Args a) {
                 for (int j = 0; j < 4; ++j) d[m] = __builtin_amdgcn_fdot2(h[j], xr[m][4 * q + j], d[m], false);
         }
 #pragma unroll
-        for (int m = 0; m < MR; ++m) part[r * MR + m] = d[m] * sc[r];
+        for (int m = 0; m < MR; ++m) part[r * MR + m] = d[m] * sc[b * R + r];
     }
     Fold<V, 32>::run(part, lane);
-    if ((lane & (64 / V - 1)) == 0) s_part[wave][fold_index<V>(lane)] = part[0];
+    if ((lane & (64 / V - 1)) == 0) s_part[wave][b * V + fold_index<V>(lane)] = part[0];
+    }
     __syncthreads();
-    if (tid < V) {
+    if (tid < B * V) {
         const int r = tid / MR, m = tid % MR;
         const int64_t n = n0 + r;
         if (n < a.columns && m < a.rows) {
@@ -1159,25 +1164,35 @@ hipError_t launch_w4a16_gemv(const W8A16Args& a, hipStream_t stream) {
     const int64_t chunks = a.width / 32;
     const int64_t T = ((chunks + 63) / 64) * 64;
     if (T > 1024) return hipErrorInvalidValue;  // the caller keeps width <= 32768
-    // Rows per workgroup: 8 measured best on MI355X for decode shapes of tens
-    // of MB and more (2 on matrices of a few MB); OMNI_W4A16_GEMV pins it.
+    // OMNI_W4A16_GEMV=<r><b> pins r rows per batch and b batches per
+    // workgroup (tuning aid); unset: the measured choice below.
     const char* ov = std::getenv("OMNI_W4A16_GEMV");
-    const int r = ov ? std::atoi(ov) : (a.columns * a.width / 2 >= (4 << 20) ? 8 : 2);
-    auto go = [&](auto rt) {
-        constexpr int R = decltype(rt)::value;
-        const dim3 grid((unsigned)((a.columns + R - 1) / R)), block((unsigned)T);
+    int cfg = ov ? std::atoi(ov) : 0;
+    // Measured on MI355X: 4 rows per workgroup from 4 MB of codes (9.8 us
+    // at 4096 x 14336), two batches of 4 from 64 MB (53 us at the 128256-row
+    // vocabulary head, against 58 for one batch of 8), 2 rows below 4 MB.
+    const int64_t code_bytes = a.columns * a.width / 2;
+    if (cfg == 0) cfg = code_bytes >= (64 << 20) ? 42 : code_bytes >= (4 << 20) ? 41 : 21;
+    auto go = [&](auto rt, auto bt) {
+        constexpr int R = decltype(rt)::value, B = decltype(bt)::value;
+        const dim3 grid((unsigned)((a.columns + R * B - 1) / (R * B))), block((unsigned)T);
         switch (a.rows) {
-            case 1: hipLaunchKernelGGL((w4a16_gemv_kernel<1, R>), grid, block, 0, stream, a); break;
-            case 2: hipLaunchKernelGGL((w4a16_gemv_kernel<2, R>), grid, block, 0, stream, a); break;
-            default: hipLaunchKernelGGL((w4a16_gemv_kernel<4, R>), grid, block, 0, stream, a); break;
+            case 1: hipLaunchKernelGGL((w4a16_gemv_kernel<1, R, B>), grid, block, 0, stream, a); break;
+            case 2: hipLaunchKernelGGL((w4a16_gemv_kernel<2, R, B>), grid, block, 0, stream, a); break;
+            default: hipLaunchKernelGGL((w4a16_gemv_kernel<4, R, B>), grid, block, 0, stream, a); break;
         }
         return hipGetLastError();
     };
-    if (r == 1) return go(std::integral_constant<int, 1>{});
-    if (r == 2) return go(std::integral_constant<int, 2>{});
-    if (r == 8) return go(std::integral_constant<int, 8>{});
-    if (r == 16) return go(std::integral_constant<int, 16>{});
-    return go(std::integral_constant<int, 4>{});
+    using std::integral_constant;
+    switch (cfg) {
+        case 11: return go(integral_constant<int, 1>{}, integral_constant<int, 1>{});
+        case 21: return go(integral_constant<int, 2>{}, integral_constant<int, 1>{});
+        case 41: return go(integral_constant<int, 4>{}, integral_constant<int, 1>{});
+        case 42: return go(integral_constant<int, 4>{}, integral_constant<int, 2>{});
+        case 44: return go(integral_constant<int, 4>{}, integral_constant<int, 4>{});
+        case 82: return go(integral_constant<int, 8>{}, integral_constant<int, 2>{});
+        default: return go(integral_constant<int, 8>{}, integral_constant<int, 1>{});
+    }
 }
 
 hipError_t launch_w4a16_skinny(const W8A16Args& a, hipStream_t stream) {

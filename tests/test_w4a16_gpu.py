@@ -62,8 +62,10 @@ def test_every_path_random(oracle, rows, width, columns, group):
     assert tolerance.rel_err(got, route) <= tolerance.FP16_REL_TOL
 
 
-@pytest.mark.parametrize("r", ["1", "2", "4", "8", "16"])
+@pytest.mark.parametrize("r", ["11", "21", "41", "81", "42", "44", "82"])
 def test_gemv_every_rows_per_workgroup(oracle, monkeypatch, r):
+    # OMNI_W4A16_GEMV=<rows per batch><batches per workgroup>; column counts
+    # leave the last workgroup's batches partly or wholly past the matrix
     monkeypatch.setenv("OMNI_W4A16_GEMV", r)
     for rows, width, columns in ((1, 4096, 37), (4, 2048, 130), (3, 96, 9)):
         rng = np.random.default_rng(rows + width + columns + int(r))
