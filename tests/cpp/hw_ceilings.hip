@@ -7,10 +7,11 @@
 //                       TOPS and the shader clock (cycle counter against the
 //                       100 MHz real-time counter) — the power-managed ceiling.
 //   hw_ceilings ladder  the W8A8 ring kernel's K loop rebuilt one ingredient at a
-//                       time, operands from LDS/L2 only: 24 MFMAs per 64-byte K
-//                       tile per wave, + 14 fragment reads, + one barrier, + 7
-//                       global->LDS copies per wave issued between MFMAs, + the
-//                       same copies issued by 4 separate producer waves.
+//                       time (MFMAs, + double-buffered fragment reads, + one
+//                       barrier, + global->LDS copies from L2, + the copies
+//                       streaming the real kernel's operands from HBM), for
+//                       128 x 96 and 128 x 128 per wave; then the fp16 ring's
+//                       K loop (+ the int8 -> f16 weight conversion).
 //   hw_ceilings read    one launch streaming 58.7 MB (the decode GEMV's weight
 //                       bytes) over 19 rotating copies, for several grid sizes:
 //                       the single-launch HBM read ceiling.
@@ -21,6 +22,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 #include <vector>
 
 #define CK(x)                                                                       \
@@ -36,6 +38,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 #define LDS_AS __attribute__((address_space(3)))
 
 // ---------------------------------------------------------------- mfma --
@@ -152,156 +156,319 @@ void run_mfma(int cus) {
 }
 
 // -------------------------------------------------------------- ladder --
-// The ring kernel's per-wave K-tile work: a 128 x 96 block of 32x32 int32
-// accumulators (4 x 3 MFMAs per 32-byte k step, two k steps per 64-byte tile),
-// fragment reads from a 4-stage LDS ring of 256 + 192 rows of 64 bytes, and
-// 7 one-KiB global->LDS copies per wave per tile from an L2-resident buffer.
-// RUNG 0: MFMAs only; 1: + fragment reads; 2: + one barrier per tile;
-// 3: + copies between MFMAs; 4: 4 more waves do the copies (512 threads).
-constexpr int kStage = (256 + 192) * 64;
-
-template <int RUNG>
-__global__ __launch_bounds__(RUNG == 4 ? 512 : 256, 1) void ladder(const uint8_t* __restrict__ src,
-                                                                   int iters, int* out,
-                                                                   unsigned long long* clk) {
+// The int8 ring kernel's per-wave K-tile work, one ingredient at a time: a
+// 128 x WN block of 32x32 int32 accumulators (two 32-byte k steps per 64-byte
+// K tile), fragments double-buffered (the reads of the next k step are issued
+// behind the current step's MFMAs, one per MFMA), and per K tile one barrier
+// and (256 + 2 WN) / 64 one-KiB global->LDS copies per wave.
+// RUNG 0: MFMAs only; 1: + fragment reads; 2: + one barrier per K tile;
+// 3: + copies from an L2-resident window; 4: the copies stream the real
+// kernel's operands instead: tile (m, n) of a 16 x 16 grid over A [4096][12288]
+// and W [16 * 2 WN][12288], random bytes, K advancing 64 bytes per tile.
+template <int WN, int RUNG>
+__global__ __launch_bounds__(256, 1) void ladder8(const uint8_t* __restrict__ src, const uint8_t* __restrict__ big,
+                                                  int iters, int* out, unsigned long long* clk) {
+    constexpr int BN = 2 * WN;
+    constexpr int kStage = (256 + BN) * 64;
+    constexpr int kCpw = (256 + BN) / 64;
+    constexpr int FM = 4, FN = WN / 32, PER = FM * FN;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[4][kStage];
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wave = wave_id & 3;
-    const bool producer = RUNG == 4 && wave_id >= 4;
-    for (int i = (tid & 255) * 16; i < 4 * kStage; i += 256 * 16) {
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    for (int i = tid * 16; i < 4 * kStage; i += 256 * 16) {
         const uint32_t h = (uint32_t)(i + blockIdx.x * 7919) * 2654435761u;
         const v4i v = {(int)h, (int)(h * 2246822519u), (int)(h * 3266489917u), (int)(h ^ 0x9e3779b9u)};
         *reinterpret_cast<v4i*>(&lds[0][0] + i) = v;
     }
     __syncthreads();
-    const int fr = lane & 31, fh = lane >> 5, fq = (fr >> 2) & 3;
     const int wm = wave >> 1, wn = wave & 1;
-    const int fa0 = (wm * 128 + fr) * 64 + ((fh ^ fq) << 4);
-    const int fa1 = (wm * 128 + fr) * 64 + (((2 + fh) ^ fq) << 4);
-    const int fb0 = 256 * 64 + (wn * 96 + fr) * 64 + ((fh ^ fq) << 4);
-    const int fb1 = 256 * 64 + (wn * 96 + fr) * 64 + (((2 + fh) ^ fq) << 4);
-    v4i fa[4], fb[3];
-    for (int i = 0; i < 4; ++i) fa[i] = *reinterpret_cast<const v4i*>(&lds[0][0] + fa0 + i * 2048);
-    for (int j = 0; j < 3; ++j) fb[j] = *reinterpret_cast<const v4i*>(&lds[0][0] + fb0 + j * 2048);
-    v16i acc[4][3] = {};
-    // Copy c of a wave: 64 lanes x 16 bytes of tile rows, from a 2 MB window.
-    const int cp_row = lane >> 2, cp_chunk = (lane & 3) ^ ((lane >> 4) & 3);
-    const uint8_t* cs = src + ((size_t)(blockIdx.x % 64) * 448 + wave * 112 + cp_row) * 64 + cp_chunk * 16;
-    (void)cs;  // used by the device pass only
+    const int fr = lane & 31, fk = lane >> 5;
+    int offA[FM], offB[FN];
+    for (int i = 0; i < FM; ++i) offA[i] = (wm * 128 + i * 32 + fr) * 64 + fk * 16;
+    for (int j = 0; j < FN; ++j) offB[j] = 256 * 64 + (wn * WN + j * 32 + fr) * 64 + fk * 16;
+    v4i fa[2][FM], fb[2][FN];
+    for (int i = 0; i < FM; ++i) fa[0][i] = fa[1][i] = *reinterpret_cast<const v4i*>(&lds[0][0] + offA[i]);
+    for (int j = 0; j < FN; ++j) fb[0][j] = fb[1][j] = *reinterpret_cast<const v4i*>(&lds[0][0] + offB[j]);
+    v16i acc[FM][FN];
+    for (int i = 0; i < FM; ++i)
+        for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
+    const int cp_row = lane >> 2, cp_chunk = lane & 3;
+    const uint8_t* cs = src + ((size_t)(blockIdx.x % 64) * 512 + wave * 128 + cp_row) * 64 + cp_chunk * 16;
+    const int tm = (blockIdx.x / 16) % 16, tn = blockIdx.x % 16;
+    const uint8_t* big_a = big + (size_t)(tm * 256) * 12288;
+    const uint8_t* big_w = big + (size_t)4096 * 12288 + (size_t)(tn * BN) * 12288;
+    const uint8_t* rsrc[kCpw];
+    for (int c = 0; c < kCpw; ++c) {
+        const int r16 = (wave * kCpw + c) * 16;
+        rsrc[c] = (r16 < 256 ? big_a + (size_t)(r16 + cp_row) * 12288
+                             : big_w + (size_t)(r16 - 256 + cp_row) * 12288) + cp_chunk * 16;
+    }
+    (void)cs;
+    (void)rsrc;
     auto copy = [&](int it, int c) {
 #if defined(__HIP_DEVICE_COMPILE__)
-        __builtin_amdgcn_global_load_lds(cs + (size_t)(it & 31) * kStage + c * 1024,
-                                         (LDS_AS void*)(&lds[(it + 3) & 3][0] + wave * 7168 + c * 1024), 16, 0, 0);
+        LDS_AS void* dst = (LDS_AS void*)(&lds[(it + 3) & 3][0] + wave * kCpw * 1024 + c * 1024);
+        if constexpr (RUNG >= 4)
+            __builtin_amdgcn_global_load_lds(rsrc[c] + (size_t)(it % 192) * 64, dst, 16, 0, 0);
+        else
+            __builtin_amdgcn_global_load_lds(cs + (size_t)(it & 31) * kStage + c * 1024, dst, 16, 0, 0);
 #endif
     };
-    const unsigned long long t0 = __builtin_readcyclecounter(), r0 = __builtin_amdgcn_s_memrealtime();
-    if (producer) {
-        for (int it = 0; it < iters; ++it) {
+    // k step s of K tile it on buffer b, reading step s + 1 into buffer b ^ 1
+    auto step = [&](int it, int s, auto bt) {
+        constexpr int b = decltype(bt)::value;
+        const int ns = s ^ 1;
+        const uint8_t* nbase = &lds[(ns == 0 ? it + 1 : it) & 3][0];
 #pragma unroll
-            for (int c = 0; c < 7; ++c) copy(it, c);
-            __builtin_amdgcn_s_waitcnt((14 & 15) | (7 << 4) | (15 << 8));  // vmcnt(14)
-            asm volatile("s_barrier" ::: "memory");
-        }
-    } else {
-        for (int it = 0; it < iters; ++it) {
-            const int st = it & 3;
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-                for (int q = 0; q < 12; ++q) {
-                    const int i = q / 3, j = q % 3;
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
-                    if constexpr (RUNG == 3)
-                        if (ks == 1 && q < 7) copy(it, q);
-                    if constexpr (RUNG >= 1)
-                        if (q < 7) {
-                            const uint8_t* base = &lds[st][0];
-                            if (q < 4)
-                                fa[q] = *reinterpret_cast<const v4i*>(base + (ks ? fa1 : fa0) + q * 2048);
-                            else
-                                fb[q - 4] = *reinterpret_cast<const v4i*>(base + (ks ? fb1 : fb0) + (q - 4) * 2048);
-                        }
-                    __builtin_amdgcn_sched_barrier(0);
+        for (int q = 0; q < PER; ++q) {
+            const int i = q / FN, j = q % FN;
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[b][i], fb[b][j], acc[i][j], 0, 0, 0);
+            if constexpr (RUNG >= 1)
+                if (q < FM + FN) {
+                    if (q < FM) fa[b ^ 1][q] = *reinterpret_cast<const v4i*>(nbase + offA[q] + ns * 32);
+                    else fb[b ^ 1][q - FM] = *reinterpret_cast<const v4i*>(nbase + offB[q - FM] + ns * 32);
                 }
-                if constexpr (RUNG >= 2)
-                    if (ks == 0) {
-                        if constexpr (RUNG == 3)
-                            __builtin_amdgcn_s_waitcnt((14 & 15) | (7 << 4) | (0 << 8));  // vmcnt(14) lgkmcnt(0)
-                        else
-                            __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
-                        asm volatile("s_barrier" ::: "memory");
-                    }
-            }
+            if constexpr (RUNG >= 3)
+                if (s == 1 && q < kCpw) copy(it, q);
+            __builtin_amdgcn_sched_barrier(0);
         }
+        if constexpr (RUNG >= 2)
+            if (s == 0) {
+                if constexpr (RUNG >= 3)
+                    __builtin_amdgcn_s_waitcnt((kCpw & 15) | (7 << 4) | (0 << 8) | ((kCpw >> 4) << 14));
+                else
+                    __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));
+                asm volatile("s_barrier" ::: "memory");
+            }
+    };
+    const unsigned long long t0 = __builtin_readcyclecounter(), r0 = __builtin_amdgcn_s_memrealtime();
+    for (int it = 0; it < iters; ++it) {
+        step(it, 0, std::integral_constant<int, 0>{});
+        step(it, 1, std::integral_constant<int, 1>{});
     }
     __builtin_amdgcn_s_waitcnt(0);
     const unsigned long long t1 = __builtin_readcyclecounter(), r1 = __builtin_amdgcn_s_memrealtime();
     int res = 0;
-    for (int i = 0; i < 4; ++i)
-        for (int j = 0; j < 3; ++j)
+    for (int i = 0; i < FM; ++i)
+        for (int j = 0; j < FN; ++j)
             for (int e = 0; e < 16; ++e) res ^= acc[i][j][e];
-    if (tid < 256) out[blockIdx.x * 256 + tid] = res;
+    out[blockIdx.x * 256 + tid] = res;
     if (tid == 0) {
         clk[blockIdx.x * 2] = t1 - t0;
         clk[blockIdx.x * 2 + 1] = r1 - r0;
     }
 }
 
+// The fp16 ring kernel's K loop (int8 weights, 128 x 128 per wave, 64-element
+// K tiles of two 32-k pairs): per pair 32 v_mfma_f32_32x32x16_f16, 8 x and 4 W
+// fragment reads for the next pair (double-buffered), per K tile one barrier
+// and 12 one-KiB copies per wave from an L2-resident window.
+// RUNG 1: MFMAs + reads; 2: + barrier; 3: + copies; 4: + the int8 -> f16
+// conversion of the next pair's W fragments, one word per MFMA slot.
+__device__ __forceinline__ v2h bits_half2(uint32_t u) {
+    v2h h;
+    __builtin_memcpy(&h, &u, 4);
+    return h;
+}
+template <int RUNG>
+__global__ __launch_bounds__(256, 1) void ladder16(const uint8_t* __restrict__ src, int iters, float* out,
+                                                   unsigned long long* clk) {
+    constexpr int kStage = 256 * 128 + 256 * 64;
+    constexpr int NB = 4, PER = 2 * NB * NB, NRA = 2 * NB, NR = 3 * NB;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[3][kStage];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    for (int i = tid * 16; i < 3 * kStage; i += 256 * 16) {
+        const uint32_t h = (uint32_t)(i + blockIdx.x * 7919) * 2654435761u;
+        const v4i v = {(int)(h & 0x3bff3bff), (int)((h * 2246822519u) & 0x3bff3bff),
+                       (int)((h * 3266489917u) & 0x3bff3bff), (int)((h ^ 0x9e3779b9u) & 0x3bff3bff)};
+        *reinterpret_cast<v4i*>(&lds[0][0] + i) = v;
+    }
+    __syncthreads();
+    const int wm = wave >> 1, wn = wave & 1;
+    const int fr = lane & 31, fk = lane >> 5;
+    int offA[NB], offB[NB];
+    for (int i = 0; i < NB; ++i) {
+        offA[i] = (wm * 128 + i * 32 + fr) * 128 + fk * 16;
+        offB[i] = 256 * 128 + (wn * 128 + i * 32 + fr) * 64 + fk * 16;
+    }
+    v8h xa[2][NB][2], bh[2][NB][2];
+    v4i xb[2][NB];
+    for (int b = 0; b < 2; ++b)
+        for (int i = 0; i < NB; ++i) {
+            xa[b][i][0] = xa[b][i][1] = *reinterpret_cast<const v8h*>(&lds[0][0] + offA[i]);
+            xb[b][i] = *reinterpret_cast<const v4i*>(&lds[0][0] + offB[i]);
+            __builtin_memcpy(&bh[b][i][0], &xb[b][i], 16);
+            bh[b][i][1] = bh[b][i][0];
+        }
+    v16f acc[NB][NB];
+    for (int i = 0; i < NB; ++i)
+        for (int j = 0; j < NB; ++j) acc[i][j] = v16f{};
+    const int cp_row = lane >> 2, cp_chunk = lane & 3;
+    const uint8_t* cs = src + ((size_t)(blockIdx.x % 64) * 768 + wave * 192 + cp_row) * 64 + cp_chunk * 16;
+    (void)cs;
+    auto copy = [&](int it, int c) {
+#if defined(__HIP_DEVICE_COMPILE__)
+        __builtin_amdgcn_global_load_lds(cs + (size_t)(it & 31) * kStage + c * 1024,
+                                         (LDS_AS void*)(&lds[(it + 2) % 3][0] + wave * 12288 + c * 1024), 16, 0, 0);
+#endif
+    };
+    auto pair = [&](int it, int s, auto bt) {
+        constexpr int b = decltype(bt)::value;
+        const int ns = s ^ 1;
+        const uint8_t* nbase = &lds[(ns == 0 ? it + 1 : it) % 3][0];
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const int half = q / (NB * NB), r = q % (NB * NB), i = r / NB, j = r % NB;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa[b][i][half], bh[b][j][half], acc[i][j], 0, 0, 0);
+            if (q < NR) {
+                if (q < NRA) {
+                    const int bi = q >> 1, hh = q & 1;
+                    xa[b ^ 1][bi][hh] =
+                        *reinterpret_cast<const v8h*>(nbase + ((offA[bi] + ns * 64 + hh * 32) & (256 * 128 - 16)));
+                } else {
+                    xb[b ^ 1][q - NRA] = *reinterpret_cast<const v4i*>(nbase + offB[q - NRA] + ns * 32);
+                }
+            }
+            if constexpr (RUNG >= 4) {
+                const int cq = q - (NR + 2);
+                if (cq >= 0 && cq < 4 * NB) {
+                    const int cj = cq >> 2, w = cq & 3;
+                    const uint32_t biased = (uint32_t)xb[b ^ 1][cj][w] ^ 0x80808080u;
+                    const v2h k1152 = {(_Float16)1152.0f, (_Float16)1152.0f};
+                    const v2h lo = bits_half2(__builtin_amdgcn_perm(0x64646464u, biased, 0x04010400u)) - k1152;
+                    const v2h hi = bits_half2(__builtin_amdgcn_perm(0x64646464u, biased, 0x04030402u)) - k1152;
+                    v8h& dst = bh[b ^ 1][cj][w >> 1];
+                    const int e = (w & 1) * 4;
+                    dst[e] = lo[0];
+                    dst[e + 1] = lo[1];
+                    dst[e + 2] = hi[0];
+                    dst[e + 3] = hi[1];
+                }
+            }
+            if constexpr (RUNG >= 3)
+                if (s == 1 && q < 12) copy(it, q);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (RUNG >= 2)
+            if (s == 0) {
+                if constexpr (RUNG >= 3)
+                    __builtin_amdgcn_s_waitcnt((12 & 15) | (7 << 4) | (0 << 8));
+                else
+                    __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));
+                asm volatile("s_barrier" ::: "memory");
+            }
+    };
+    const unsigned long long t0 = __builtin_readcyclecounter(), r0 = __builtin_amdgcn_s_memrealtime();
+    for (int it = 0; it < iters; ++it) {
+        pair(it, 0, std::integral_constant<int, 0>{});
+        pair(it, 1, std::integral_constant<int, 1>{});
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    const unsigned long long t1 = __builtin_readcyclecounter(), r1 = __builtin_amdgcn_s_memrealtime();
+    float res = 0;
+    for (int i = 0; i < NB; ++i)
+        for (int j = 0; j < NB; ++j)
+            for (int e = 0; e < 16; ++e) res += acc[i][j][e];
+    out[blockIdx.x * 256 + tid] = res;
+    if (tid == 0) {
+        clk[blockIdx.x * 2] = t1 - t0;
+        clk[blockIdx.x * 2 + 1] = r1 - r0;
+    }
+}
+
+template <typename F>
+float time_launches(F launch) {
+    launch();
+    CK(hipGetLastError());
+    CK(hipDeviceSynchronize());
+    hipEvent_t a, b;
+    CK(hipEventCreate(&a));
+    CK(hipEventCreate(&b));
+    CK(hipEventRecord(a));
+    for (int r = 0; r < 5; ++r) launch();
+    CK(hipEventRecord(b));
+    CK(hipEventSynchronize(b));
+    float ms;
+    CK(hipEventElapsedTime(&ms, a, b));
+    return ms / 5;
+}
+
+double mean_cycles(const std::vector<unsigned long long>& c, int n) {
+    double cyc = 0;
+    for (int i = 0; i < n; ++i) cyc += (double)c[2 * i];
+    return cyc / n;
+}
+
+template <int WN, int RUNG>
+void run_ladder8_case(const uint8_t* src, const uint8_t* big, int* out, unsigned long long* clk, int cus) {
+    const int iters = 1920;
+    const float ms = time_launches(
+        [&] { hipLaunchKernelGGL((ladder8<WN, RUNG>), dim3(cus), dim3(256), 0, 0, src, big, iters, out, clk); });
+    std::vector<unsigned long long> c((size_t)cus * 2);
+    CK(hipMemcpy(c.data(), clk, c.size() * 8, hipMemcpyDeviceToHost));
+    const double ops = (double)cus * 4 * iters * 2.0 * 128 * WN * 64;
+    const double mfma_cycles = (double)iters * 128 * WN * 64 * 2 / 2048.0;  // 2048 int8 ops / clk / SIMD
+    const char* names[] = {"MFMAs only", "+ fragment reads", "+ barrier per K tile", "+ copies (L2-resident)",
+                           "copies stream A/W from HBM"};
+    printf("ladder8 wave 128x%d rung %d %-28s: %6.0f TOPS  clock %5.0f MHz  MFMA busy %5.1f%%\n", WN, RUNG,
+           names[RUNG], ops / (ms * 1e-3) / 1e12, mean_mhz(c, cus), 100.0 * mfma_cycles / mean_cycles(c, cus));
+    fflush(stdout);
+}
+
+template <int RUNG>
+void run_ladder16_case(const uint8_t* src, float* out, unsigned long long* clk, int cus) {
+    const int iters = 1000;
+    const float ms =
+        time_launches([&] { hipLaunchKernelGGL((ladder16<RUNG>), dim3(cus), dim3(256), 0, 0, src, iters, out, clk); });
+    std::vector<unsigned long long> c((size_t)cus * 2);
+    CK(hipMemcpy(c.data(), clk, c.size() * 8, hipMemcpyDeviceToHost));
+    const double flops = (double)cus * 4 * iters * 2.0 * 128 * 128 * 64;
+    const double mfma_cycles = (double)iters * 2.0 * 128 * 128 * 64 / 1024.0;  // 1024 f16 flops / clk / SIMD
+    const char* names[] = {"", "MFMAs + fragment reads", "+ barrier per K tile", "+ copies (L2-resident)",
+                           "+ int8->f16 conversion"};
+    printf("ladder16 wave 128x128 rung %d %-24s: %6.0f TFLOP/s  clock %5.0f MHz  MFMA busy %5.1f%%\n", RUNG,
+           names[RUNG], flops / (ms * 1e-3) / 1e12, mean_mhz(c, cus), 100.0 * mfma_cycles / mean_cycles(c, cus));
+    fflush(stdout);
+}
+
 void run_ladder(int cus) {
-    // 64 windows of 448 rows, plus 32 K tiles of stride: every copy stays inside.
-    const size_t bytes = (size_t)64 * 448 * 64 + (size_t)32 * kStage + 4096;
-    std::vector<uint8_t> h(bytes);
+    const size_t bytes = (size_t)64 * 768 * 64 + (size_t)32 * (256 * 128 + 256 * 64) + 4096;
+    const size_t big_bytes = (size_t)(4096 + 16 * 256) * 12288;
+    std::vector<uint8_t> h(big_bytes);
     uint32_t s = 1;
     for (auto& b : h) {
         s = s * 1664525u + 1013904223u;
         b = (uint8_t)(s >> 24);
     }
-    uint8_t* src;
+    uint8_t *src, *big;
     int* out;
     unsigned long long* clk;
     CK(hipMalloc(&src, bytes));
+    CK(hipMalloc(&big, big_bytes));
     CK(hipMalloc(&out, (size_t)cus * 256 * 4));
     CK(hipMalloc(&clk, (size_t)cus * 16));
     CK(hipMemcpy(src, h.data(), bytes, hipMemcpyHostToDevice));
-    const int iters = 4000;
-    const char* names[] = {"MFMAs only", "+ LDS fragment reads", "+ barrier per K tile",
-                           "+ 7 LDS-DMA copies/wave between MFMAs", "copies by 4 producer waves"};
-    for (int rep = 0; rep < 2; ++rep)
-        for (int rung = 0; rung < 5; ++rung) {
-            auto launch = [&] {
-                switch (rung) {
-                    case 0: hipLaunchKernelGGL(ladder<0>, dim3(cus), dim3(256), 0, 0, src, iters, out, clk); break;
-                    case 1: hipLaunchKernelGGL(ladder<1>, dim3(cus), dim3(256), 0, 0, src, iters, out, clk); break;
-                    case 2: hipLaunchKernelGGL(ladder<2>, dim3(cus), dim3(256), 0, 0, src, iters, out, clk); break;
-                    case 3: hipLaunchKernelGGL(ladder<3>, dim3(cus), dim3(256), 0, 0, src, iters, out, clk); break;
-                    default: hipLaunchKernelGGL(ladder<4>, dim3(cus), dim3(512), 0, 0, src, iters, out, clk);
-                }
-            };
-            launch();
-            CK(hipGetLastError());
-            CK(hipDeviceSynchronize());
-            hipEvent_t a, b;
-            CK(hipEventCreate(&a));
-            CK(hipEventCreate(&b));
-            CK(hipEventRecord(a));
-            for (int r = 0; r < 5; ++r) launch();
-            CK(hipEventRecord(b));
-            CK(hipEventSynchronize(b));
-            float ms;
-            CK(hipEventElapsedTime(&ms, a, b));
-            ms /= 5;
-            std::vector<unsigned long long> c((size_t)cus * 2);
-            CK(hipMemcpy(c.data(), clk, c.size() * 8, hipMemcpyDeviceToHost));
-            double cyc = 0;
-            for (int i = 0; i < cus; ++i) cyc += (double)c[2 * i];
-            cyc /= cus;
-            const double mfmas = (double)iters * 24;
-            printf("ladder pass %d rung %d %-40s: %6.0f TOPS  clock %5.0f MHz  %5.1f cycles/MFMA  MFMA busy %5.1f%%\n",
-                   rep, rung, names[rung], (double)cus * 4 * mfmas * 65536 / (ms * 1e-3) / 1e12,
-                   mean_mhz(c, cus), cyc / mfmas, 3200.0 / (cyc / mfmas));
-        }
+    CK(hipMemcpy(big, h.data(), big_bytes, hipMemcpyHostToDevice));
+    for (int rep = 0; rep < 2; ++rep) {
+        run_ladder8_case<96, 0>(src, big, out, clk, cus);
+        run_ladder8_case<96, 1>(src, big, out, clk, cus);
+        run_ladder8_case<96, 2>(src, big, out, clk, cus);
+        run_ladder8_case<96, 3>(src, big, out, clk, cus);
+        run_ladder8_case<96, 4>(src, big, out, clk, cus);
+        run_ladder8_case<128, 3>(src, big, out, clk, cus);
+        run_ladder8_case<128, 4>(src, big, out, clk, cus);
+    }
+    // fp16 operands: bytes with the f16 exponent field kept finite
+    CK(hipMemset(src, 0x3b, bytes));
+    for (int rep = 0; rep < 2; ++rep) {
+        run_ladder16_case<1>(src, reinterpret_cast<float*>(out), clk, cus);
+        run_ladder16_case<2>(src, reinterpret_cast<float*>(out), clk, cus);
+        run_ladder16_case<3>(src, reinterpret_cast<float*>(out), clk, cus);
+        run_ladder16_case<4>(src, reinterpret_cast<float*>(out), clk, cus);
+    }
     CK(hipFree(src));
+    CK(hipFree(big));
     CK(hipFree(out));
     CK(hipFree(clk));
 }
