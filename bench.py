@@ -420,6 +420,13 @@ def configs_bench(torch, oi, gen, dev, stream, steps):
                       "TOPS": round(ops / t / 1e12, 1)})
     res["4_dit_convrot_layers"] = rows4
 
+    # The floor under every launch: a graph of 400 launches of a 1 x 64 -> 1
+    # GEMV (launch, dispatch and completion of an almost empty kernel).
+    xt = torch.randn((1, 64), generator=gen, device=dev).half()
+    wt = torch.ones((1, 64), device=dev, dtype=torch.int8)
+    st = torch.ones(1, device=dev).half()
+    res["launch_floor_us"] = round(timed(lambda: oi.w8a16_linear(xt, wt, st), 400) * 1e6, 3)
+
     # 5: small-VLM mix: 28 layers of (q, kv, o, gate, up, down), W8A16.
     H, F, KV, L = 1536, 8960, 512, 28
     dims = ((H, H), (H, KV), (H, H), (H, F), (H, F), (F, H))  # (K, N) per linear
