@@ -13,8 +13,9 @@
 //                       128 x 96 and 128 x 128 per wave; then the fp16 ring's
 //                       K loop (+ the int8 -> f16 weight conversion).
 //   hw_ceilings read    one launch streaming 58.7 MB (the decode GEMV's weight
-//                       bytes) over 19 rotating copies, for several grid sizes:
-//                       the single-launch HBM read ceiling.
+//                       bytes) over 19 rotating copies, every load of a thread
+//                       issued up front, for several loads per thread and
+//                       block sizes: the single-launch HBM read ceiling.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -474,55 +475,79 @@ void run_ladder(int cus) {
 }
 
 // ---------------------------------------------------------------- read --
-__global__ __launch_bounds__(256) void stream_read(const uint4* __restrict__ p, int64_t n16, unsigned* out) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    unsigned x = 0;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) {
-        const uint4 v = p[i];
-        x ^= v.x ^ v.y ^ v.z ^ v.w;
+// Each thread issues U nontemporal 16-byte loads before using any; a block of
+// T threads covers T * U consecutive chunks (load u of thread t: chunk
+// block * T * U + u * T + t), the access pattern of the GEMV's weight loads.
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+template <int U>
+__global__ __launch_bounds__(1024) void stream_read(const v4u* __restrict__ p, int64_t n16, unsigned* out) {
+    const int64_t base = (int64_t)blockIdx.x * blockDim.x * U + threadIdx.x;
+    v4u v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        int64_t i = base + (int64_t)u * blockDim.x;
+        i = i < n16 ? i : n16 - 1;
+        v[u] = __builtin_nontemporal_load(p + i);
     }
+    unsigned x = 0;
+#pragma unroll
+    for (int u = 0; u < U; ++u) x ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
     if (x == 0x12345678u) out[0] = x;  // keeps the loads
+}
+
+template <int U>
+void run_read_case(const v4u* buf, int64_t n16, int copies, unsigned* out, hipStream_t s, int T) {
+    const int64_t grid = (n16 + (int64_t)T * U - 1) / ((int64_t)T * U);
+    const int iters = copies * 10;
+    hipGraph_t g;
+    hipGraphExec_t ge;
+    CK(hipStreamBeginCapture(s, hipStreamCaptureModeGlobal));
+    for (int i = 0; i < iters; ++i)
+        hipLaunchKernelGGL((stream_read<U>), dim3((unsigned)grid), dim3(T), 0, s, buf + (int64_t)(i % copies) * n16,
+                           n16, out);
+    CK(hipStreamEndCapture(s, &g));
+    CK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+    CK(hipGraphLaunch(ge, s));
+    CK(hipStreamSynchronize(s));
+    float best = 1e30f;
+    for (int rep = 0; rep < 3; ++rep) {
+        hipEvent_t a, b;
+        CK(hipEventCreate(&a));
+        CK(hipEventCreate(&b));
+        CK(hipEventRecord(a, s));
+        CK(hipGraphLaunch(ge, s));
+        CK(hipEventRecord(b, s));
+        CK(hipEventSynchronize(b));
+        float ms;
+        CK(hipEventElapsedTime(&ms, a, b));
+        best = std::min(best, ms);
+    }
+    const double us = best * 1000.0 / iters;
+    printf("read 58.7 MB per launch, %2d loads per thread, block %4d, grid %6lld: %6.2f us  %5.0f GB/s\n", U, T,
+           (long long)grid, us, n16 * 16 / us / 1e3);
+    fflush(stdout);
+    CK(hipGraphExecDestroy(ge));
+    CK(hipGraphDestroy(g));
 }
 
 void run_read() {
     const int64_t bytes = 4096LL * 14336, n16 = bytes / 16;
     const int copies = 19;
-    uint4* buf;
+    v4u* buf;
     unsigned* out;
     CK(hipMalloc(&buf, bytes * copies));
     CK(hipMalloc(&out, 64));
     CK(hipMemset(buf, 1, bytes * copies));
     hipStream_t s;
     CK(hipStreamCreate(&s));
-    for (int grid : {512, 1024, 2048, 4096, 8192}) {
-        const int iters = copies * 10;
-        hipGraph_t g;
-        hipGraphExec_t ge;
-        CK(hipStreamBeginCapture(s, hipStreamCaptureModeGlobal));
-        for (int i = 0; i < iters; ++i)
-            hipLaunchKernelGGL(stream_read, dim3(grid), dim3(256), 0, s, buf + (int64_t)(i % copies) * n16, n16, out);
-        CK(hipStreamEndCapture(s, &g));
-        CK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
-        CK(hipGraphLaunch(ge, s));
-        CK(hipStreamSynchronize(s));
-        float best = 1e30f;
-        for (int rep = 0; rep < 3; ++rep) {
-            hipEvent_t a, b;
-            CK(hipEventCreate(&a));
-            CK(hipEventCreate(&b));
-            CK(hipEventRecord(a, s));
-            CK(hipGraphLaunch(ge, s));
-            CK(hipEventRecord(b, s));
-            CK(hipEventSynchronize(b));
-            float ms;
-            CK(hipEventElapsedTime(&ms, a, b));
-            best = std::min(best, ms);
-        }
-        const double us = best * 1000.0 / iters;
-        printf("read 58.7 MB per launch, grid %5d x 256: %6.2f us  %5.0f GB/s\n", grid, us, bytes / us / 1e3);
-        CK(hipGraphExecDestroy(ge));
-        CK(hipGraphDestroy(g));
+    for (int T : {256, 512, 1024}) {
+        run_read_case<1>(buf, n16, copies, out, s, T);
+        run_read_case<2>(buf, n16, copies, out, s, T);
+        run_read_case<4>(buf, n16, copies, out, s, T);
+        run_read_case<8>(buf, n16, copies, out, s, T);
+        run_read_case<16>(buf, n16, copies, out, s, T);
     }
+    CK(hipStreamDestroy(s));
     CK(hipFree(buf));
     CK(hipFree(out));
 }
