@@ -817,9 +817,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a16_mfma_kernel(W
 // WB = 16 (the fp16 linear): W is f16 and staged like x, as two [BN][64-byte]
 // halves, and its fragments are read like x's (two ds_read_b128 per pair);
 // there is no scale.
-template <int BM, int BN, int WB = 8, int WMW = 2>
+template <int BM, int BN, int WB = 8, int WMW = 2, int S = 3>
 __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
-    constexpr int S = 3;
+    static_assert(S == 2 || S == 3, "2 or 3 stages");
     constexpr int WNW = 4 / WMW;              // waves along N
     constexpr int WM = BM / WMW, WN = BN / WNW;
     constexpr int FM = WM / 32, FN = WN / 32;
@@ -830,10 +830,10 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     constexpr int kFrags = 2 * FM + kWH * FN; // fragment reads per pair
     static_assert(kRows % 64 == 0 && FM >= 1 && FN >= 1, "tile shape");
     static_assert(kCpw <= 2 * FM * FN && kFrags <= 2 * FM * FN, "one read and copy per MFMA slot");
-    static_assert(3 * kStage + 4 * BN * 4 <= 160 * 1024, "LDS");
+    static_assert(S * kStage + 4 * BN * 4 <= 160 * 1024, "LDS");
     __shared__ __attribute__((aligned(1024))) uint8_t st0[kStage];
     __shared__ __attribute__((aligned(1024))) uint8_t st1[kStage];
-    __shared__ __attribute__((aligned(1024))) uint8_t st2[kStage];
+    __shared__ __attribute__((aligned(1024))) uint8_t st2[S > 2 ? kStage : 1024];
     __shared__ float sScale[2][BN];
     __shared__ float sBias[2][BN];
 
@@ -849,7 +849,7 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     const bool has_bias = a.bias != nullptr;
     constexpr int kGroupM = 4;
     auto stage = [&](int s) -> uint8_t* { return s == 0 ? st0 : s == 1 ? st1 : st2; };
-    const unsigned stage_lds[3] = {lds_addr(st0), lds_addr(st1), lds_addr(st2)};
+    const unsigned stage_lds[3] = {lds_addr(st0), lds_addr(st1), S > 2 ? lds_addr(st2) : 0u};
 
     // Copy c fills stage rows 16c .. 16c+15; lane l reads logical chunk
     // (l % 4) ^ ((l / 16) % 4) of row l / 4, landing at physical chunk l % 4.
@@ -937,19 +937,18 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     // back-to-back MFMAs into one accumulator would serialise).
     v16f acc[FM][FN];
     auto pair_mfmas = [&](v4i (&xa)[FM][2], v4i (&xb)[FN][kWH], auto&& after) {
-        v8h bh[FN][2];
+        // f16 weights (WB = 16) feed the MFMA straight from their fragment
+        // registers; int8 weights are converted into bh first.
+        v8h bh[WB == 8 ? FN : 1][2];
+        if constexpr (WB == 8) {
 #pragma unroll
-        for (int jn = 0; jn < FN; ++jn) {
-            if constexpr (WB == 8) {
+            for (int jn = 0; jn < FN; ++jn) {
                 const u32 wd[4] = {(u32)xb[jn][0][0], (u32)xb[jn][0][1], (u32)xb[jn][0][2], (u32)xb[jn][0][3]};
                 v2h h[8];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) i8x4_to_f16x4(wd[q], h[2 * q], h[2 * q + 1]);
                 bh[jn][0] = v8h{h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
                 bh[jn][1] = v8h{h[4][0], h[4][1], h[5][0], h[5][1], h[6][0], h[6][1], h[7][0], h[7][1]};
-            } else {
-                __builtin_memcpy(&bh[jn][0], &xb[jn][0], 16);
-                __builtin_memcpy(&bh[jn][1], &xb[jn][kWH - 1], 16);
             }
         }
 #pragma unroll
@@ -958,9 +957,13 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
             for (int jn = 0; jn < FN; ++jn) {
 #pragma unroll
                 for (int i = 0; i < FM; ++i) {
-                    v8h av;
+                    v8h av, bv;
                     __builtin_memcpy(&av, &xa[i][half], 16);
-                    acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bh[jn][half], acc[i][jn], 0, 0, 0);
+                    if constexpr (WB == 8)
+                        bv = bh[jn][half];
+                    else
+                        __builtin_memcpy(&bv, &xb[jn][half * (kWH - 1)], 16);
+                    acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc[i][jn], 0, 0, 0);
                     after(half * FM * FN + jn * FM + i);
                     __builtin_amdgcn_sched_barrier(0);
                 }
@@ -1076,7 +1079,7 @@ bool ring16_fits(const W8A16Args& a) {
            a.columns < (int64_t(1) << 23);
 }
 
-template <int BM, int BN, int WB = 8, int WMW = 2>
+template <int BM, int BN, int WB = 8, int WMW = 2, int S = 3>
 hipError_t launch_ring16_cfg(const W8A16Args& a, hipStream_t stream) {
     const int64_t tiles = ((a.rows + BM - 1) / BM) * ((a.columns + BN - 1) / BN);
     int dev = 0, cus = 256;
@@ -1084,7 +1087,7 @@ hipError_t launch_ring16_cfg(const W8A16Args& a, hipStream_t stream) {
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         cus = 256;
     const int64_t grid = tiles < cus ? tiles : cus;
-    hipLaunchKernelGGL((w8a16_ring_kernel<BM, BN, WB, WMW>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((w8a16_ring_kernel<BM, BN, WB, WMW, S>), dim3((unsigned)grid), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 
