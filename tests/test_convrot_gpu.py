@@ -61,8 +61,12 @@ def check_codes(codes, scale, total, r_ref, oracle_scale):
     assert np.array_equal(total, got.sum(axis=1))
 
 
+# widths of 1-64 groups take the packed-rows kernel (1-4 waves, 1-16 rows per
+# workgroup); wider rows take the four-wave two-pass kernel (81 groups: two
+# passes, the second mostly idle)
 @pytest.mark.parametrize("rows,width", [(1, 256), (7, 512), (33, 3072), (5, 4096), (3, 2304),
-                                        (4, 4352), (2, 12288), (1, 16384)])
+                                        (4, 4352), (2, 12288), (1, 16384), (37, 256), (9, 768),
+                                        (3, 20736)])
 @pytest.mark.parametrize("dtype", [np.float16, np.float32])
 def test_fused_rotation_quantisation_matches_the_oracle(oracle, rows, width, dtype):
     rng = np.random.default_rng(rows * 7 + width)
