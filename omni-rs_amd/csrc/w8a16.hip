@@ -51,6 +51,15 @@ __device__ __forceinline__ void i8x4_to_f16x4(u32 word, v2h& lo, v2h& hi) {
     hi = bits_half2(p1) - k1152;
 }
 
+// The same four codes as the f16 values 1152 + w (exact): three VALU per
+// four codes. A dot product against them exceeds the true one by 1152 * (the
+// sum of the activations), which the caller subtracts once per row.
+__device__ __forceinline__ void i8x4_to_f16x4_biased(u32 word, v2h& lo, v2h& hi) {
+    const u32 biased = word ^ 0x80808080u;
+    lo = bits_half2(__builtin_amdgcn_perm(0x64646464u, biased, 0x04010400u));
+    hi = bits_half2(__builtin_amdgcn_perm(0x64646464u, biased, 0x04030402u));
+}
+
 // Eight int4 codes of `word` (low nibble first, each stored plus 8, as
 // crates/minicpm-v/src/quant.rs:22-29 unpacks them) -> four f16 pairs in k
 // order (n0,n1) (n2,n3) (n4,n5) (n6,n7), exact: bytes [n, 0x64] are the f16
@@ -63,6 +72,21 @@ __device__ __forceinline__ void i4x8_to_f16x8(u32 word, v2h (&h)[4]) {
     h[1] = bits_half2(__builtin_amdgcn_perm(hi, lo, 0x0C050C01u) | 0x64006400u) - k1032;
     h[2] = bits_half2(__builtin_amdgcn_perm(hi, lo, 0x0C060C02u) | 0x64006400u) - k1032;
     h[3] = bits_half2(__builtin_amdgcn_perm(hi, lo, 0x0C070C03u) | 0x64006400u) - k1032;
+}
+
+// Eight int4 codes of `word` as the f16 values 1024 + nibble (exact), one
+// v_perm_b32 per pair placing a nibble byte under the high byte 0x64 taken
+// from k64 = 0x64646464, in the pairs (n0, n2), (n1, n3), (n4, n6), (n5, n7).
+// The codes are nibble - 8, so a dot product against these values exceeds
+// the true one by 1032 * (the sum of the activations), which the caller
+// subtracts once per row of partial sums instead of once per pair.
+__device__ __forceinline__ void i4x8_to_f16x8_biased(u32 word, u32 k64, v2h (&h)[4]) {
+    const u32 lo = word & 0x0F0F0F0Fu;         // n0 n2 n4 n6
+    const u32 hi = (word >> 4) & 0x0F0F0F0Fu;  // n1 n3 n5 n7
+    h[0] = bits_half2(__builtin_amdgcn_perm(k64, lo, 0x04010400u));
+    h[1] = bits_half2(__builtin_amdgcn_perm(k64, hi, 0x04010400u));
+    h[2] = bits_half2(__builtin_amdgcn_perm(k64, lo, 0x04030402u));
+    h[3] = bits_half2(__builtin_amdgcn_perm(k64, hi, 0x04030402u));
 }
 
 // A bf16 scale (quant.rs:74-81) as f32 (exact) and as f16 (exact for scales
@@ -181,6 +205,25 @@ __global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
         }
     }
 
+    // With more weight rows than activation rows per lane, codes enter the
+    // dot products as 1152 + w (three VALU per four codes, not five) and
+    // each row's partial sum drops xc = 1152 * sum(x), accumulated in the
+    // same order. Products are exact and the f32 sums stay below
+    // 2^11 * sum|x|: ~1e-5 of the result relative, nothing on integer data.
+    constexpr bool kBiased = WB == 8 && RB > MR;
+    float xc[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        xc[m] = 0.0f;
+        if constexpr (kBiased) {
+            const v2h k1152 = {(_Float16)1152.0f, (_Float16)1152.0f};
+#pragma unroll
+            for (int j = 0; j < CPL; ++j)
+#pragma unroll
+                for (int e = 0; e < kP; ++e) xc[m] = __builtin_amdgcn_fdot2(k1152, xr[j][m][e], xc[m], false);
+        }
+    }
+
     // Then every weight load. Rows past the matrix and chunks past K are
     // clamped, not predicated (a predicated load lets the compiler pull its
     // consumers next to it); clamped chunks meet zero activations.
@@ -221,7 +264,10 @@ __global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
             for (int q = 0; q < 4; ++q) {
                 if constexpr (WB == 8) {
                     v2h w01, w23;
-                    i8x4_to_f16x4(words[q], w01, w23);
+                    if constexpr (kBiased)
+                        i8x4_to_f16x4_biased(words[q], w01, w23);
+                    else
+                        i8x4_to_f16x4(words[q], w01, w23);
 #pragma unroll
                     for (int m = 0; m < MR; ++m) {
                         float& p = part[r * MR + m];
@@ -237,6 +283,12 @@ __global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
                 }
             }
         }
+    }
+    if constexpr (kBiased) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) part[r * MR + m] -= xc[m];
     }
     Fold<V, 32>::run(part, lane);
     if ((lane & (64 / V - 1)) == 0) s_part[wave][b * V + fold_index<V>(lane)] = part[0];
@@ -453,9 +505,14 @@ hipError_t launch_skinny(const W8A16Args& a, hipStream_t stream) {
 
 // Decode GEMV (rows <= 4) for int4 weights: the W8A16 GEMV's design with 32
 // codes (16 bytes) per lane per row: a lane's 32-value chunk lies in one
-// scale group (group % 32 == 0), so the chunk's dot is taken on the exact
-// codes and multiplied by its scale once. A workgroup of T = 64 * ceil(K /
-// 2048) lanes owns R weight rows; every weight load is issued up front.
+// scale group (group % 32 == 0), so the chunk's dot is taken on the codes
+// (with more weight rows than activation rows per lane: as 1024 + nibble,
+// less 1032 * sum(x) once per chunk, four VALU per eight codes fewer than
+// exact decoding) and multiplied by its scale once. Products
+// are exact and the f32 sums stay below 2^13 * sum|x|, so the correction
+// costs ~1e-4 of the result relative and nothing on integer data. A
+// workgroup of T = 64 * ceil(K / 2048) lanes owns R weight rows; every weight
+// load is issued up front.
 template <int MR, int R, int B = 1>
 __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W8A16Args a) {
     constexpr int V = R * MR;
@@ -472,8 +529,17 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W8A16Args a) {
     const bool live = tid < chunks;
     const int64_t c = live ? tid : chunks - 1;  // clamped: meets zero activations
 
-    // x: 32 halves of each row's chunk as 16 f16 pairs.
+    // x: 32 halves of each row's chunk as 16 f16 pairs, in the order of
+    // i4x8_to_f16x8_biased's weight pairs: (x0, x2), (x1, x3), (x4, x6),
+    // (x5, x7) of every eight; xc = 1032 * (their sum), accumulated in the
+    // same pair order as the dot products it corrects.
+    // The re-pairing and xc cost 32 VALU per activation row and save 16 per
+    // weight row, so they pay when a lane has more weight rows than
+    // activation rows; otherwise x keeps its order and codes are exact.
+    constexpr bool kBiased = RB > MR;
     v2h xr[MR][16];
+    float xc[MR];
+    const v2h k1032 = {(_Float16)1032.0f, (_Float16)1032.0f};
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
         if (live && m < a.rows) {
@@ -481,16 +547,29 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W8A16Args a) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const uint4 v = p[q];
-                xr[m][4 * q] = bits_half2(v.x);
-                xr[m][4 * q + 1] = bits_half2(v.y);
-                xr[m][4 * q + 2] = bits_half2(v.z);
-                xr[m][4 * q + 3] = bits_half2(v.w);
+                if constexpr (kBiased) {
+                    xr[m][4 * q] = bits_half2(__builtin_amdgcn_perm(v.y, v.x, 0x05040100u));
+                    xr[m][4 * q + 1] = bits_half2(__builtin_amdgcn_perm(v.y, v.x, 0x07060302u));
+                    xr[m][4 * q + 2] = bits_half2(__builtin_amdgcn_perm(v.w, v.z, 0x05040100u));
+                    xr[m][4 * q + 3] = bits_half2(__builtin_amdgcn_perm(v.w, v.z, 0x07060302u));
+                } else {
+                    xr[m][4 * q] = bits_half2(v.x);
+                    xr[m][4 * q + 1] = bits_half2(v.y);
+                    xr[m][4 * q + 2] = bits_half2(v.z);
+                    xr[m][4 * q + 3] = bits_half2(v.w);
+                }
             }
         } else {
 #pragma unroll
             for (int e = 0; e < 16; ++e) xr[m][e] = v2h{};
         }
+        xc[m] = 0.0f;
+        if constexpr (kBiased) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) xc[m] = __builtin_amdgcn_fdot2(k1032, xr[m][e], xc[m], false);
+        }
     }
+    const u32 k64 = 0x64646464u;
     v4u wv[RB];
     float sc[RB];
 #pragma unroll
@@ -519,14 +598,17 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W8A16Args a) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             v2h h[4];
-            i4x8_to_f16x8(words[q], h);
+            if constexpr (kBiased)
+                i4x8_to_f16x8_biased(words[q], k64, h);
+            else
+                i4x8_to_f16x8(words[q], h);
 #pragma unroll
             for (int m = 0; m < MR; ++m)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) d[m] = __builtin_amdgcn_fdot2(h[j], xr[m][4 * q + j], d[m], false);
         }
 #pragma unroll
-        for (int m = 0; m < MR; ++m) part[r * MR + m] = d[m] * sc[b * R + r];
+        for (int m = 0; m < MR; ++m) part[r * MR + m] = (d[m] - xc[m]) * sc[b * R + r];
     }
     Fold<V, 32>::run(part, lane);
     if ((lane & (64 / V - 1)) == 0) s_part[wave][b * V + fold_index<V>(lane)] = part[0];
