@@ -359,10 +359,14 @@ hipError_t launch_gemv_m(const W8A16Args& a, hipStream_t stream) {
     // Measured on MI355X over the BASELINE decode shapes: 64 bytes of weights
     // in flight per lane, two chunks per lane once a row is wider than 512
     // chunks, and more, smaller workgroups when the whole matrix is a few MB.
-    // Four activation rows: 16 rows per workgroup in two batches of 8 (x is
-    // then re-read from L2 for one eighth of the weight bytes, not a half),
-    // 10-15 % faster than 8 rows on the 14336- and 128256-row shapes.
+    // Four activation rows: two batches per workgroup (x is then re-read
+    // from L2 for a fraction of the weight bytes): batches of 4 rows up to
+    // 512 chunks and 64 M weights (17 % faster than batches of 8 at
+    // 4096 x 4096, 5 % at 4096 x 14336), batches of 8 beyond (the 128256-row
+    // head, K = 14336).
     if (a.columns * a.width <= (4 << 20)) return launch_gemv_cfg<MR, 2, 1, WB>(a, stream);
+    if (MR == 4 && chunks <= 512 && a.columns * a.width <= (64 << 20))
+        return launch_gemv_cfg<MR, 1, 4, WB, 2>(a, stream);
     if (MR == 4 && chunks <= 1024) return launch_gemv_cfg<MR, 1, 8, WB, 2>(a, stream);
     if (chunks > 512) return launch_gemv_cfg<MR, 2, 4, WB>(a, stream);
     return launch_gemv_cfg<MR, 1, 4, WB>(a, stream);
