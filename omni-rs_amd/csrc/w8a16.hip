@@ -903,14 +903,19 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a16_mfma_kernel(W
 // WB = 16 (the fp16 linear): W is f16 and staged like x, as two [BN][64-byte]
 // halves, and its fragments are read like x's (two ds_read_b128 per pair);
 // there is no scale.
-template <int BM, int BN, int WB = 8, int WMW = 2, int S = 3>
+// KP = 1 (f16 weights only): K tiles of 32 elements, one MFMA pair each, so
+// a stage is half as large and a 256 x 256 tile fits three of them.
+template <int BM, int BN, int WB = 8, int WMW = 2, int S = 3, int KP = 2>
 __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     static_assert(S == 2 || S == 3, "2 or 3 stages");
+    static_assert(KP == 2 || (KP == 1 && WB == 16), "32-element K tiles need f16 weights");
     constexpr int WNW = 4 / WMW;              // waves along N
     constexpr int WM = BM / WMW, WN = BN / WNW;
     constexpr int FM = WM / 32, FN = WN / 32;
-    constexpr int kWH = WB / 8;               // 64-byte W rows per column per K tile
-    constexpr int kRows = 2 * BM + kWH * BN;  // 64-byte stage rows: x k 0..31, x k 32..63, W
+    constexpr int kWH = WB / 8;               // 64-byte W rows per column per 64 K
+    constexpr int kXR = KP;                   // 64-byte x rows per row per K tile
+    constexpr int kWR = KP == 2 ? kWH : 1;    // 64-byte W rows per column per K tile
+    constexpr int kRows = kXR * BM + kWR * BN;  // 64-byte stage rows: x k 0..31 (, x k 32..63), W
     constexpr int kStage = kRows * 64;
     constexpr int kCpw = kRows / 64;          // 1 KiB copies per wave per K tile
     constexpr int kFrags = 2 * FM + kWH * FN; // fragment reads per pair
@@ -931,7 +936,7 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     const int tiles_n = (int)((a.columns + BN - 1) / BN);
     const int total = tiles_m * tiles_n;
     const int64_t K = a.width;
-    const int ktiles = (int)(K / 64);
+    const int ktiles = (int)(K / (32 * KP));
     const bool has_bias = a.bias != nullptr;
     constexpr int kGroupM = 4;
     auto stage = [&](int s) -> uint8_t* { return s == 0 ? st0 : s == 1 ? st1 : st2; };
@@ -958,12 +963,12 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
 #pragma unroll
         for (int j = 0; j < kCpw; ++j) {
             const int c16 = (wave * kCpw + j) * 16;  // wave-uniform
-            if (c16 < 2 * BM) {
+            if (c16 < kXR * BM) {
                 const int half = c16 >= BM;
                 const int64_t row = min(m0 + (c16 - half * BM) + cp_row, a.rows - 1);
                 voff[j] = (unsigned)(row * K * 2) + half * 64 + cp_chunk * 16;
             } else {
-                const int rel = c16 - 2 * BM;
+                const int rel = c16 - kXR * BM;
                 const int half = WB == 16 && rel >= BN;
                 const int64_t row = min(n0 + (rel - half * BN) + cp_row, a.columns - 1);
                 voff[j] = (unsigned)(row * K * kWH) + half * 64 + cp_chunk * 16;
@@ -985,9 +990,9 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     };
     auto copy_one = [&](int kt, int s, int j) {
         const int64_t kk = min(kt, ktiles - 1);
-        const bool is_x = (wave * kCpw + j) * 16 < 2 * BM;  // wave-uniform
-        const uint8_t* base = is_x ? reinterpret_cast<const uint8_t*>(a.x) + kk * 128
-                                   : reinterpret_cast<const uint8_t*>(a.w) + kk * 64 * kWH;
+        const bool is_x = (wave * kCpw + j) * 16 < kXR * BM;  // wave-uniform
+        const uint8_t* base = is_x ? reinterpret_cast<const uint8_t*>(a.x) + kk * 64 * KP
+                                   : reinterpret_cast<const uint8_t*>(a.w) + kk * 32 * KP * kWH;
         lds_copy16_saddr(voff[j], base, stage_lds[s] + (wave * kCpw + j) * 1024);
     };
     auto copy_tile = [&](int kt, int s) {
@@ -998,9 +1003,9 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     // Fragment offsets within a stage.
     const int fr = lane & 31, fh = lane >> 5, fq = (fr >> 2) & 3;
     auto offA = [&](int p, int j) { return (p * BM + wm * WM + fr) * 64 + (((2 * fh + j) ^ fq) << 4); };
-    auto offB = [&](int p) { return (2 * BM + wn * WN + fr) * 64 + (((2 * p + fh) ^ fq) << 4); };
+    auto offB = [&](int p) { return (kXR * BM + wn * WN + fr) * 64 + (((2 * p + fh) ^ fq) << 4); };
     auto offB16 = [&](int p, int j) {
-        return (2 * BM + p * BN + wn * WN + fr) * 64 + (((2 * fh + j) ^ fq) << 4);
+        return (kXR * BM + p * BN + wn * WN + fr) * 64 + (((2 * fh + j) ^ fq) << 4);
     };
     v4i xa0[FM][2], xb0[FN][kWH], xa1[FM][2], xb1[FN][kWH];
     // Fragment idx of a pair: A (i, j) for idx < 2 FM, else B idx - 2 FM
@@ -1085,22 +1090,52 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
 #pragma unroll
         for (int idx = 0; idx < kFrags; ++idx) read_frag(0, 0, idx, xa0, xb0);
 
-        for (int t0 = 0; t0 < ktiles; t0 += S) {
+        if constexpr (KP == 2) {
+            for (int t0 = 0; t0 < ktiles; t0 += S) {
 #pragma unroll
-            for (int u = 0; u < S; ++u) {
-                const int kt = t0 + u;
-                if (kt < ktiles) {  // uniform across the workgroup
-                    // Pair 0 of tile kt; reads of pair 1.
-                    pair_mfmas(xa0, xb0, [&](int q) {
-                        if (q < kFrags) read_frag(u, 1, q, xa1, xb1);
-                    });
-                    s_waitcnt_vm<(S - 2) * kCpw, true>();
-                    lds_barrier();  // tile kt+1 landed everywhere; stage u is read
-                    // Pair 1 of tile kt; copies of tile kt+S into stage u; reads of tile kt+1, pair 0.
-                    pair_mfmas(xa1, xb1, [&](int q) {
-                        if (q < kCpw) copy_one(kt + S, u, q);
-                        if (q < kFrags) read_frag((u + 1) % S, 0, q, xa0, xb0);
-                    });
+                for (int u = 0; u < S; ++u) {
+                    const int kt = t0 + u;
+                    if (kt < ktiles) {  // uniform across the workgroup
+                        // Pair 0 of tile kt; reads of pair 1.
+                        pair_mfmas(xa0, xb0, [&](int q) {
+                            if (q < kFrags) read_frag(u, 1, q, xa1, xb1);
+                        });
+                        s_waitcnt_vm<(S - 2) * kCpw, true>();
+                        lds_barrier();  // tile kt+1 landed everywhere; stage u is read
+                        // Pair 1 of tile kt; copies of tile kt+S into stage u; reads of tile kt+1, pair 0.
+                        pair_mfmas(xa1, xb1, [&](int q) {
+                            if (q < kCpw) copy_one(kt + S, u, q);
+                            if (q < kFrags) read_frag((u + 1) % S, 0, q, xa0, xb0);
+                        });
+                    }
+                }
+            }
+        } else {
+            // One pair per K tile; the fragment buffers alternate by tile, so
+            // the unrolled body covers 2 S tiles (stage kt % S, buffer kt % 2).
+            for (int t0 = 0; t0 < ktiles; t0 += 2 * S) {
+#pragma unroll
+                for (int u2 = 0; u2 < 2 * S; ++u2) {
+                    const int kt = t0 + u2;
+                    const int u = u2 % S;
+                    if (kt < ktiles) {  // uniform across the workgroup
+                        // Tile kt's fragments were read during tile kt-1: once
+                        // tile kt+1 has landed and every wave has passed here,
+                        // stage u may be refilled with tile kt+S.
+                        s_waitcnt_vm<(S - 2) * kCpw, true>();
+                        lds_barrier();
+                        if (u2 % 2 == 0) {
+                            pair_mfmas(xa0, xb0, [&](int q) {
+                                if (q < kCpw) copy_one(kt + S, u, q);
+                                if (q < kFrags) read_frag((u + 1) % S, 0, q, xa1, xb1);
+                            });
+                        } else {
+                            pair_mfmas(xa1, xb1, [&](int q) {
+                                if (q < kCpw) copy_one(kt + S, u, q);
+                                if (q < kFrags) read_frag((u + 1) % S, 0, q, xa0, xb0);
+                            });
+                        }
+                    }
                 }
             }
         }
@@ -1165,7 +1200,7 @@ bool ring16_fits(const W8A16Args& a) {
            a.columns < (int64_t(1) << 23);
 }
 
-template <int BM, int BN, int WB = 8, int WMW = 2, int S = 3>
+template <int BM, int BN, int WB = 8, int WMW = 2, int S = 3, int KP = 2>
 hipError_t launch_ring16_cfg(const W8A16Args& a, hipStream_t stream) {
     const int64_t tiles = ((a.rows + BM - 1) / BM) * ((a.columns + BN - 1) / BN);
     int dev = 0, cus = 256;
@@ -1173,7 +1208,7 @@ hipError_t launch_ring16_cfg(const W8A16Args& a, hipStream_t stream) {
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         cus = 256;
     const int64_t grid = tiles < cus ? tiles : cus;
-    hipLaunchKernelGGL((w8a16_ring_kernel<BM, BN, WB, WMW, S>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((w8a16_ring_kernel<BM, BN, WB, WMW, S, KP>), dim3((unsigned)grid), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -1329,12 +1364,20 @@ hipError_t launch_f16_mfma(const W8A16Args& a, hipStream_t stream) {
         case 4: if (ring_ok) return launch_ring16_cfg<256, 128, 16>(a, stream); break;
         case 5: if (ring_ok) return launch_ring16_cfg<128, 128, 16>(a, stream); break;
         case 6: if (ring_ok) return launch_ring16_cfg<128, 256, 16>(a, stream); break;
+        case 7: if (ring_ok) return launch_ring16_cfg<256, 256, 16, 2, 3, 1>(a, stream); break;
+        case 8: if (ring_ok) return launch_ring16_cfg<256, 128, 16, 2, 3, 1>(a, stream); break;
         default: break;
     }
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         cus = 256;
+    // 256 x 256 tiles on 32-element K tiles once they fill a round of CUs
+    // (4096 x 4096 x 12288: 373 us against 442 for 256 x 128; half the LDS
+    // reads per flop), else 256 x 128 on 64-element K tiles.
+    const int64_t wide_tiles = ((a.rows + 255) / 256) * ((a.columns + 255) / 256);
+    if (ring_ok && a.width >= 3072 && wide_tiles >= cus)
+        return launch_ring16_cfg<256, 256, 16, 2, 3, 1>(a, stream);
     const int64_t ring_tiles = ((a.rows + 255) / 256) * ((a.columns + 127) / 128);
     if (ring_ok && a.width >= 3072 && ring_tiles >= cus) return launch_ring16_cfg<256, 128, 16>(a, stream);
     const int64_t big_tiles = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
