@@ -125,10 +125,13 @@ __device__ __forceinline__ void lds_copy16(const uint8_t* src, uint8_t* lds_dst)
 // flight, so it inserts no vmcnt wait of its own before a later LDS read
 // (where it cannot tell which ring stage a copy targets it waits for every
 // outstanding operation, a full pipeline drain per K tile). The caller's
-// explicit waits order the copies. lds_dst must be wave-uniform.
-// The same, addressed as a wave-uniform 64-bit base (SGPRs) plus a 32-bit
-// per-lane byte offset (no per-lane 64-bit pointer is held or added), and
-// with the LDS byte address given as a wave-uniform integer (see lds_addr).
+// explicit waits order the copies. The source is a wave-uniform 64-bit base
+// (SGPRs) plus a 32-bit per-lane byte offset (no per-lane 64-bit pointer is
+// held or added); the LDS byte address is a wave-uniform integer (see
+// lds_addr). m0 is listed as clobbered, which the compiler reports as a
+// reserved register it will not preserve: a kernel that uses this copy must
+// not also use the builtin lds_copy16 (whose m0 setup the compiler may hoist);
+// the only other m0 users on gfx950 are absent from these kernels.
 __device__ __forceinline__ void lds_copy16_saddr(unsigned voff, const void* base, unsigned lds_byte) {
 #if defined(__HIP_DEVICE_COMPILE__)
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds_byte)
@@ -143,12 +146,6 @@ __device__ __forceinline__ unsigned lds_addr(const void* p) {
 #else
     (void)p;
     return 0;
-#endif
-}
-__device__ __forceinline__ void lds_copy16_asm(const void* src, void* lds_dst) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(OMNI_LDS void*)lds_dst);
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
 #endif
 }
 
