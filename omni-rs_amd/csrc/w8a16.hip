@@ -1258,6 +1258,7 @@ hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream) {
         case 5: if (ring_ok) return launch_ring16_cfg<128, 128>(a, stream); break;
         case 6: if (ring_ok) return launch_ring16_cfg<256, 256>(a, stream); break;
         case 7: if (ring_ok) return launch_ring16_cfg<256, 256, 8, 1>(a, stream); break;
+        case 8: if (ring_ok) return launch_ring16_cfg<64, 128>(a, stream); break;
         default: break;
     }
     // Measured on MI355X (config 5 and the BASELINE GEMM shapes): the ring
@@ -1276,8 +1277,15 @@ hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream) {
     const int64_t ring_tiles = ((a.rows + 255) / 256) * ((a.columns + 127) / 128);
     if (ring_ok && a.width >= 3072 && ring_tiles >= cus) return launch_ring16_cfg<256, 128>(a, stream);
     // Smaller prefill shapes (config 5's M = 1024 linears, K 1536 and 8960):
-    // the 128 x 128 ring beats the register-staged tiled kernels by 10-35 %.
-    if (ring_ok) return launch_ring16_cfg<128, 128>(a, stream);
+    // the 128 x 128 ring beats the register-staged tiled kernels by 10-35 %;
+    // where even twice its tile count fits in one round of CUs, 64 x 128
+    // tiles keep more CUs busy (1024 x 8960 -> 1536: 54.5 us against 66.8,
+    // 1024 x 1536 -> 1536: 13.4 against 16.6).
+    if (ring_ok) {
+        const int64_t tiles128 = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
+        if (2 * tiles128 <= cus) return launch_ring16_cfg<64, 128>(a, stream);
+        return launch_ring16_cfg<128, 128>(a, stream);
+    }
     const int64_t big_tiles = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
     if (big_tiles >= 512) return launch_mfma16_cfg<128, 128, 64, 2, 2, 4>(a, stream);
     return launch_mfma16_cfg<64, 64, 64, 2, 2, 4>(a, stream);

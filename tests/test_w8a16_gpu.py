@@ -144,13 +144,13 @@ def test_skinny_rows_on_both_routes(oracle, monkeypatch, route, rows, width, col
     assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL, (route, rows, width, columns)
 
 
-@pytest.mark.parametrize("tile", ["1", "2", "4", "5", "6", "7"])
+@pytest.mark.parametrize("tile", ["1", "2", "4", "5", "6", "7", "8"])
 @pytest.mark.parametrize("rows,width,columns", [(300, 512, 200), (1024, 1536, 1536), (257, 8960, 129),
                                                 (197, 4096, 640), (65, 64, 33), (600, 4096, 700)])
 def test_every_prefill_kernel(oracle, monkeypatch, tile, rows, width, columns):
     # OMNI_W8A16_TILE pins one prefill kernel: the tiled GEMMs (1, 2) and the
     # LDS-DMA ring GEMMs (4 = 256 x 128, 5 = 128 x 128, 6 = 256 x 256, 7 = 256 x 256
-    # with the waves side by side); ragged rows/columns,
+    # with the waves side by side, 8 = 64 x 128); ragged rows/columns,
     # bias, against the f64 ground truth
     monkeypatch.setenv("OMNI_W8A16_TILE", tile)
     rng = np.random.default_rng(rows + width + columns + int(tile))
