@@ -127,7 +127,9 @@ int omni_try_int8_gemm(const void* x, int x_dtype, int64_t rows, int64_t width,
  *   then codes, row scales and row sums of r as omni_int8_quantize_rows.
  * r is computed in f32 by a fast transform, not by a 256-term dot: its
  * rounding differs from the reference's f32 matmul by a few ulp, so a code
- * can differ by one where r / row_scale lies within that of k + 0.5.
+ * can differ by one where r / row_scale lies within that of k + 0.5. The
+ * quotient and the half-add of the rounding are one fused rounding, which
+ * moves codes only inside that same band (within 2 ulp of k + 0.5).
  * group must be 256 (convrot.rs:12), width % 256 == 0 (convrot.rs:39-43),
  * else OMNI_NOT_HANDLED; x and every row start (ld_x) 16-byte aligned,
  * x_packed 16-byte aligned. x_sum may be NULL. */
