@@ -574,17 +574,20 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W8A16Args a) {
         }
     }
     const u32 k64 = 0x64646464u;
+    // The group scales are loaded before the weights: memory operations
+    // retire in order, so a scale issued after every weight row would hold
+    // row 0's arithmetic until the last row had landed.
     v4u wv[RB];
     float sc[RB];
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
         const int64_t n = n0 + r < a.columns ? n0 + r : a.columns - 1;
-        wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(a.w + n * (K / 2) + c * 16));
+        sc[r] = bf16_to_f32(a.gscale[n * gpr + (c * 32) / a.group]);
     }
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
         const int64_t n = n0 + r < a.columns ? n0 + r : a.columns - 1;
-        sc[r] = bf16_to_f32(a.gscale[n * gpr + (c * 32) / a.group]);
+        wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(a.w + n * (K / 2) + c * 16));
     }
     const int64_t n_ep = min(n0 + (tid / MR) % RB, a.columns - 1);
     const _Float16 bi_h = a.bias ? a.bias[n_ep] : (_Float16)0.0f;
