@@ -48,47 +48,7 @@ def parse():
                         "that scales rocprofv3's FETCH_SIZE / WRITE_SIZE readings")
     p.add_argument("--configs-only", action="store_true",
                    help="only time every BASELINE.json config (one JSON line)")
-    p.add_argument("--gemm-data-sweep", action="store_true",
-                   help="only time the W8A8 GEMM of both north_star shapes on random and on "
-                        "constant operands (same kernels, same work): the card's power-managed "
-                        "clock follows operand bit toggling")
     return p.parse_args()
-
-
-def gemm_data_sweep(steps):
-    """The GEMM alone (quantised codes resident) on random codes and weights,
-    then on all-ones codes and weights, then random again; one JSON line."""
-    import torch
-    import omni_int8 as oi
-    dev = torch.device("cuda:0")
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(0)
-    stream = torch.cuda.current_stream(dev)
-    res = []
-    for M, K, N in GEMM_SHAPES:
-        rs = torch.rand(M, generator=gen, device=dev) * 0.01 + 0.001
-        total = torch.zeros(M, dtype=torch.int32, device=dev)
-        scale = torch.rand(N, generator=gen, device=dev) * 0.018 + 0.002
-        zero = torch.zeros(N, dtype=torch.int32, device=dev)
-        for kind in ("random", "ones", "random"):
-            if kind == "random":
-                codes = torch.randint(-127, 128, (M, K), generator=gen, device=dev, dtype=torch.int8)
-                w = torch.randint(-127, 128, (N, K), generator=gen, device=dev, dtype=torch.int8)
-            else:
-                codes = torch.ones((M, K), device=dev, dtype=torch.int8)
-                w = torch.ones((N, K), device=dev, dtype=torch.int8)
-
-            def one():
-                oi.w8a8_gemm(codes, rs, total, w, scale, zero)
-
-            for _ in range(10):
-                one()
-            g = graph_of(one, steps)
-            t = timed_graph(g, stream) / steps
-            del g
-            res.append({"M": M, "K": K, "N": N, "operands": kind, "gemm_us": round(t * 1e6, 2),
-                        "gemm_tops": round(2.0 * M * N * K / t / 1e12, 1)})
-    print(json.dumps({"gemm_data_sweep": res}))
 
 
 def copy_calibration():
@@ -146,9 +106,31 @@ def load_traffic():
         return json.load(f)
 
 
+def host_cpu():
+    """The host this process runs on: logical CPUs, the CPUs this process may
+    use, and the CPU model."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return {"nproc": os.cpu_count(), "usable_cpus": usable, "model": model}
+
+
 def cpu_baseline(oracle, np, seconds):
-    """Reference CPU path (C restatement of int8_host::gemm, 1 thread) on the
-    first rows of the north_star GEMM, growing the sample until `seconds`."""
+    """Reference CPU path (C restatement of int8_host::gemm) on the first rows
+    of the north_star GEMM, growing the sample until `seconds`: on one thread
+    (the reference is single-threaded) and, for scale, on every CPU this
+    process may use (at most 16, the box's share) with the same per-row code
+    spread over OpenMP threads."""
     M, K, N = GEMM_SHAPES[0]
     rng = np.random.default_rng(0)
     w = rng.integers(-127, 128, (N, K), dtype=np.int8)
@@ -162,10 +144,25 @@ def cpu_baseline(oracle, np, seconds):
         elapsed += time.perf_counter() - t0
         rows += 2
     ops = 2.0 * rows * N * K
+    host = host_cpu()
+    threads = max(1, min(16, host["usable_cpus"]))
+    mt_rows, mt_elapsed = 0, 0.0
+    while mt_elapsed < seconds / 2 and mt_rows < M:
+        x = rng.standard_normal((4 * threads, K)).astype(np.float16).astype(np.float32)
+        t0 = time.perf_counter()
+        oracle.int8_gemm_threads(x, w, scale, zero, threads)
+        mt_elapsed += time.perf_counter() - t0
+        mt_rows += x.shape[0]
+    mt_ops = 2.0 * mt_rows * N * K
     return {"value": ops / elapsed / 1e12, "unit": "TOPS", "cores": 1, "kind": "port",
             "sample": f"{rows} rows of M={M},K={K},N={N} (f16 x -> int8 codes, int32 acc, "
                       f"f32 epilogue), {elapsed:.1f} s single-thread C restatement of "
-                      f"int8_host.rs:19-53"}
+                      f"int8_host.rs:19-53",
+            "host": host,
+            "all_cores": {"value": mt_ops / mt_elapsed / 1e12, "unit": "TOPS", "cores": threads,
+                          "kind": "port",
+                          "sample": f"{mt_rows} rows of the same GEMM, {mt_elapsed:.1f} s, the same "
+                                    f"restatement with rows spread over {threads} OpenMP threads"}}
 
 
 def cpu_gemv_baseline(oracle, np, seconds):
@@ -184,7 +181,72 @@ def cpu_gemv_baseline(oracle, np, seconds):
         cols += 256
     return {"value": cols * K / elapsed / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"{cols} of {N} output channels at M={M},K={K} (int8 weights streamed), "
-                      f"{elapsed:.1f} s single-thread C restatement"}
+                      f"{elapsed:.1f} s single-thread C restatement", "host": host_cpu()}
+
+
+def step_parity(oracle, np, torch, cases, step_outs, rows_per_shape=6):
+    """After timing: the f32 output of the last timed step, per shape, on
+    sampled rows (first, last and random ones) against the CPU oracle's
+    restatement of the reference CPU path, bit for bit."""
+    rng = np.random.default_rng(123)
+    res = []
+    for c, (k, out) in zip(cases, step_outs):
+        M = c["M"]
+        idx = np.unique(np.concatenate([[0, M - 1], rng.choice(M, rows_per_shape, replace=False)]))
+        it = torch.from_numpy(idx).to(out.device)
+        x = c["xs"][k].index_select(0, it).float().cpu().numpy()
+        got = out.index_select(0, it).cpu().numpy()
+        want = oracle.int8_gemm(x, c["ws"][k].cpu().numpy(), c["scale"].cpu().numpy(),
+                                c["zero"].cpu().numpy())
+        equal = bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
+        res.append({"M": M, "K": c["K"], "N": c["N"], "rows_checked": int(idx.size),
+                    "bit_exact": equal})
+        if not equal:
+            raise SystemExit(f"bench output differs from the oracle at M={M},K={c['K']},N={c['N']}")
+    return res
+
+
+def reference_shape_context(torch, oi, dev, stream, steps):
+    """The reference's own published int8 GEMM shapes (m x n x k = 256 x
+    4096 x 4096, 256 x 12288 x 4096, 256 x 4096 x 12288; its matmul2d on an
+    Apple M5 Max: 0.171 / 0.943 / 0.595 ms, int32 out) on this GPU's W8A8
+    GEMM (f32 out, fused epilogue), on the reference's own deterministic
+    operands (scripts/bench_qwen_tensorops_int8.mm:46-47), with its sampled
+    int32-dot exactness check (:65-79) on the accumulators. Cross-hardware
+    context only: different chips, and this GEMM also applies the epilogue."""
+    res = []
+    for m, n, k, m5_ms in ((256, 4096, 4096, 0.171), (256, 12288, 4096, 0.943),
+                           (256, 4096, 12288, 0.595)):
+        a = ((torch.arange(m * k, device=dev, dtype=torch.int64) * 31 + 11) % 251 - 125)
+        b = ((torch.arange(n * k, device=dev, dtype=torch.int64) * 17 + 3) % 241 - 120)
+        a = a.to(torch.int8).reshape(m, k)
+        b = b.to(torch.int8).reshape(n, k)
+        rs = torch.ones(m, device=dev)
+        ws = torch.ones(n, device=dev)
+
+        def one():
+            oi.w8a8_gemm(a, rs, None, b, ws)
+
+        for _ in range(3):
+            one()
+        g = graph_of(one, steps)
+        t = timed_graph(g, stream) / steps
+        del g
+        _, acc = oi.w8a8_gemm(a, rs, None, b, ws, acc_dump=True)
+        torch.cuda.synchronize()
+        worst = 0
+        for sidx in range(32):
+            row = m - 1 if sidx == 31 else (sidx * 997) % m
+            col = n - 1 if sidx == 31 else (sidx * 619) % n
+            dot = int((a[row].to(torch.int64) * b[col].to(torch.int64)).sum().item())
+            worst = max(worst, abs(int(acc[row, col].item()) - dot))
+        del acc
+        res.append({"m": m, "n": n, "k": k, "us": round(t * 1e6, 2),
+                    "TOPS": round(2.0 * m * n * k / t / 1e12, 1),
+                    "sampled_dot_max_abs_err": worst,
+                    "reference_m5max_matmul2d_ms": m5_ms,
+                    "note": "cross-hardware context (Apple M5 Max, int32 out, no epilogue)"})
+    return res
 
 
 def w4a16_bench(torch, oi, gen, dev, stream, steps):
@@ -493,9 +555,6 @@ def main():
         print(json.dumps({"configs": configs_bench(torch, oi, gen, dev,
                                                    torch.cuda.current_stream(dev), args.steps)}))
         return
-    if args.gemm_data_sweep:
-        gemm_data_sweep(args.steps)
-        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(the path shards by output columns across GPUs, see DESIGN.md)", file=sys.stderr)
@@ -514,53 +573,87 @@ def main():
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
 
-    # ---- W8A8: inputs resident in HBM --------------------------------------
+    # ---- W8A8: inputs resident in HBM, rotated past the MALL ---------------
+    # Each shape keeps `copies` distinct activation/weight sets (>= 1 GiB in
+    # all, >= 4 sets) and every step uses the next one, so no launch finds
+    # its operands in the 256 MB Infinity Cache from an earlier launch.
     cases = []
     for M, K, N in GEMM_SHAPES:
-        x = torch.randn((M, K), generator=gen, device=dev, dtype=torch.float32).half()
-        w = torch.randint(-127, 128, (N, K), generator=gen, device=dev, dtype=torch.int8)
-        w_packed = w.view(torch.int32).reshape(-1)
+        copies = max(4, -(-GEMV_ROTATION_BYTES // (2 * M * K + N * K + M * K)))
+        xs, ws, codes = [], [], []
+        for _ in range(copies):
+            x = torch.randn((M, K), generator=gen, device=dev, dtype=torch.float32).half()
+            w = torch.randint(-127, 128, (N, K), generator=gen, device=dev, dtype=torch.int8)
+            xs.append(x)
+            ws.append(w)
+            codes.append(oi.quantize_rows(x))
         scale = torch.rand(N, generator=gen, device=dev) * 0.018 + 0.002
         zero = torch.zeros(N, dtype=torch.int32, device=dev)
-        codes, rs, total = oi.quantize_rows(x)
-        cases.append(dict(M=M, K=K, N=N, x=x, w=w, w_packed=w_packed, scale=scale, zero=zero,
-                          codes=codes, rs=rs, total=total))
+        cases.append(dict(M=M, K=K, N=N, copies=copies, xs=xs, ws=ws, codes=codes, scale=scale,
+                          zero=zero, next=0))
 
     outs = [None] * len(cases)
+    used = [0] * len(cases)
 
     def step():
         for i, c in enumerate(cases):
-            outs[i] = oi.try_int8_gemm(c["x"], c["w_packed"], c["scale"], c["zero"])
+            k = c["next"] % c["copies"]
+            c["next"] += 1
+            used[i] = k
+            outs[i] = oi.try_int8_gemm(c["xs"][k], c["ws"][k].view(torch.int32).reshape(-1),
+                                       c["scale"], c["zero"])
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    eager = [o.clone() for o in outs]
     g_steps = graph_of(step, args.steps)
     stream = torch.cuda.current_stream(dev)
     t_steps = timed_graph(g_steps, stream)
-    for o, e in zip(outs, eager):  # the replayed graph reproduces the eager result
-        assert torch.equal(o, e), "graph replay differs from eager try_int8_gemm"
+    # The replayed graph reproduces the eager result on the copies its last
+    # step used.
+    last = list(used)
+    for i, c in enumerate(cases):
+        k = last[i]
+        eager = oi.try_int8_gemm(c["xs"][k], c["ws"][k].view(torch.int32).reshape(-1), c["scale"],
+                                 c["zero"])
+        assert torch.equal(outs[i].view(torch.int32), eager.view(torch.int32)), \
+            "graph replay differs from eager try_int8_gemm"
+    step_outs = [(last[i], outs[i].clone()) for i in range(len(cases))]
     del g_steps
     ops_per_step = sum(2.0 * c["M"] * c["N"] * c["K"] for c in cases)
     tops = ops_per_step * args.steps / t_steps / 1e12
 
-    # dominant kernel alone: the GEMM on pre-quantised codes, per orientation
+    # Dominant kernel alone: the GEMM on pre-quantised codes, per orientation,
+    # over the rotated copies (the roofline figure) and on one resident copy
+    # (for comparison: what the MALL would add).
     gemm_time = 0.0
     per_shape = []
     for c in cases:
         def one(c=c):
-            oi.w8a8_gemm(c["codes"], c["rs"], c["total"], c["w"], c["scale"], c["zero"])
+            k = c["next"] % c["copies"]
+            c["next"] += 1
+            q, rs, total = c["codes"][k]
+            oi.w8a8_gemm(q, rs, total, c["ws"][k], c["scale"], c["zero"])
 
-        for _ in range(3):
-            one()
-        g = graph_of(one, args.steps)
-        t = timed_graph(g, stream) / args.steps
-        del g
+        def resident(c=c):
+            q, rs, total = c["codes"][0]
+            oi.w8a8_gemm(q, rs, total, c["ws"][0], c["scale"], c["zero"])
+
+        times = {}
+        for name, fn in (("rotated", one), ("resident", resident)):
+            for _ in range(3):
+                fn()
+            g = graph_of(fn, args.steps)
+            times[name] = timed_graph(g, stream) / args.steps
+            del g
+        t = times["rotated"]
         gemm_time += t
-        per_shape.append({"M": c["M"], "K": c["K"], "N": c["N"], "gemm_us": round(t * 1e6, 2),
-                          "gemm_tops": round(2.0 * c["M"] * c["N"] * c["K"] / t / 1e12, 1)})
+        per_shape.append({"M": c["M"], "K": c["K"], "N": c["N"], "copies": c["copies"],
+                          "gemm_us": round(t * 1e6, 2),
+                          "gemm_tops": round(2.0 * c["M"] * c["N"] * c["K"] / t / 1e12, 1),
+                          "gemm_us_one_resident_copy": round(times["resident"] * 1e6, 2)})
     gemm_tops = ops_per_step / gemm_time / 1e12
+    context = reference_shape_context(torch, oi, dev, stream, args.steps)
     traffic = load_traffic()
 
     # ---- W8A16 GEMV over rotating weight copies ---------------------------------
@@ -600,6 +693,7 @@ def main():
     # ---- CPU baselines (oracle, bounded samples) -----------------------------
     import oracle_lib
     oracle = oracle_lib.Oracle()
+    parity = step_parity(oracle, np, torch, cases, step_outs)
     cpu = cpu_baseline(oracle, np, args.cpu_seconds)
     cpu_gemv = cpu_gemv_baseline(oracle, np, max(2.0, args.cpu_seconds / 2))
 
@@ -615,7 +709,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic: x ~ N(0,1) f16, W ~ U[-127,127] int8, scales ~ U[0.002,0.02]",
+        "data": "synthetic: x ~ N(0,1) f16, W ~ U[-127,127] int8, scales ~ U[0.002,0.02]; "
+                "each step takes the next of >= 4 operand copies (>= 1 GiB per shape)",
         "config": {"workload": "try_int8_gemm (quantize_rows + W8A8 GEMM, f32 out) at "
                                "M=4096,K=3072,N=12288 and M=4096,K=12288,N=3072",
                    "gemm_shapes": per_shape},
@@ -624,6 +719,8 @@ def main():
                      "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
                      "traffic": traffic.get("w8a8_gemm")},
         "cpu_baseline": cpu,
+        "parity": parity,
+        "reference_shapes": context,
         "gemv": {
             "metric": "W8A16 GEMV HBM GB/s", "value": round(gemv_gbs, 1), "unit": "GB/s",
             "config": {"M": gM, "K": gK, "N": gN, "weight_copies": copies,

@@ -51,10 +51,11 @@ enum omni_dtype {
 
 /* W8A8 GEMM lowering selection for omni_w8a8_gemm / omni_try_int8_gemm.
  * Replaces crates/omni-kernel/src/int8_tensorops.rs:15-24 (matmul2d_lowered /
- * enabled: OMNI_CONVROT_TENSOROPS=0 forces the scalar kernel). Here the
- * environment variable OMNI_INT8_FORCE_SCALAR=1, read once per process,
- * forces the scalar v_dot4 kernel; otherwise the int8-MFMA kernel runs
- * whenever width % 16 == 0 and the scalar kernel otherwise. */
+ * enabled). The reference's switch OMNI_CONVROT_TENSOROPS=0 forces the
+ * scalar kernel here too, as does OMNI_INT8_FORCE_SCALAR=1; both are read on
+ * every call, as the reference reads its variable. Otherwise the int8-MFMA
+ * kernel runs whenever width % 16 == 0 and the scalar v_dot4 kernel
+ * otherwise. */
 enum omni_w8a8_lowering {
     OMNI_LOWERING_AUTO = 0,
     OMNI_LOWERING_MFMA = 1,
@@ -68,7 +69,8 @@ enum omni_w8a8_lowering {
 int omni_int8_arch_supported(int device);
 
 /* Lowering that omni_w8a8_gemm would pick for this width (after the
- * OMNI_INT8_FORCE_SCALAR override). Mirrors int8_tensorops.rs:15-20. */
+ * OMNI_CONVROT_TENSOROPS=0 / OMNI_INT8_FORCE_SCALAR=1 overrides). Mirrors
+ * int8_tensorops.rs:15-20. */
 int omni_w8a8_lowering(int64_t width);
 
 /* Message for the last non-OK status returned on this thread. */

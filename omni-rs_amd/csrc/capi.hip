@@ -62,14 +62,15 @@ int check_current_device() {
     return OMNI_OK;
 }
 
-// OMNI_INT8_FORCE_SCALAR=1 forces the scalar kernel, read once per process
-// (the reference reads OMNI_CONVROT_TENSOROPS=0, int8_tensorops.rs:15-24).
+// The scalar lowering is forced by the reference's own switch,
+// OMNI_CONVROT_TENSOROPS=0 (matmul2d_lowered, int8_tensorops.rs:15-20, which
+// reads it on every call), or by OMNI_INT8_FORCE_SCALAR=1; both are read on
+// every call, as the reference does.
 bool force_scalar() {
-    static const bool value = [] {
-        const char* v = std::getenv("OMNI_INT8_FORCE_SCALAR");
-        return v && v[0] == '1';
-    }();
-    return value;
+    const char* tensorops = std::getenv("OMNI_CONVROT_TENSOROPS");
+    if (tensorops && std::strcmp(tensorops, "0") == 0) return true;
+    const char* v = std::getenv("OMNI_INT8_FORCE_SCALAR");
+    return v && v[0] == '1';
 }
 
 bool aligned(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }

@@ -30,6 +30,16 @@ __device__ __forceinline__ int quantize_code(float value) {
     return (int)signed_v;
 }
 
+// f32 -> int32 by v_cvt_i32_f32, which the ISA defines to truncate toward
+// zero, saturate to the int32 range and return 0 for NaN. A C++ (int) cast
+// of NaN or of an out-of-range value is undefined (LLVM's fptosi gives
+// poison), so the instruction is issued directly.
+__device__ __forceinline__ int cvt_i32_sat(float v) {
+    int r;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+
 // Sum of the four sign-extended bytes of a word.
 __device__ __forceinline__ int sum4(u32 word) {
     return (int)(int8_t)(word) + (int)(int8_t)(word >> 8) + (int)(int8_t)(word >> 16) +
@@ -71,7 +81,7 @@ __device__ __forceinline__ float div_rn(float x, float s, float y) {
 //
 // Rounding: trunc(q + copysign(0.5, q)) equals sign(q) * floor(|q| + 0.5)
 // with the same f32 addition as the reference (q - 0.5 is exactly
-// -(|q| + 0.5)), and v_cvt_i32_f32 truncates toward zero and maps NaN to 0.
+// -(|q| + 0.5)), and cvt_i32_sat truncates toward zero and maps NaN to 0.
 // |q| <= 127 * (1 + 2^-23) always (the row scale is the peak / 127), so the
 // clamp to [-128, 127] only ever matters for NaN/Inf-derived values.
 template <bool TINY>
@@ -80,7 +90,7 @@ __device__ __forceinline__ u32 pack4(const float* v, float s, float y, int& sum)
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
         const float q = div_rn<TINY>(v[b], s, y);
-        const int r = (int)(q + __builtin_copysignf(0.5f, q));
+        const int r = cvt_i32_sat(q + __builtin_copysignf(0.5f, q));
         c[b] = r < -128 ? -128 : (r > 127 ? 127 : r);
     }
     const u32 lo = __builtin_amdgcn_perm((u32)c[1], (u32)c[0], 0x0c0c0400u);  // c0.b0, c1.b0

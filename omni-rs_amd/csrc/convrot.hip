@@ -167,7 +167,7 @@ __device__ __forceinline__ RowQuot row_quot(float peak_u) {
 __device__ __forceinline__ u32 pack4_rot(const float* u, const RowQuot& rq, int& sum) {
     int c[4];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) c[b] = (int)__builtin_fmaf(u[b], rq.y16, __builtin_copysignf(0.5f, u[b]));
+    for (int b = 0; b < 4; ++b) c[b] = cvt_i32_sat(__builtin_fmaf(u[b], rq.y16, __builtin_copysignf(0.5f, u[b])));
     const u32 lo = __builtin_amdgcn_perm((u32)c[1], (u32)c[0], 0x0c0c0400u);  // c0.b0, c1.b0
     const u32 hi = __builtin_amdgcn_perm((u32)c[3], (u32)c[2], 0x0c0c0400u);  // c2.b0, c3.b0
     const u32 word = __builtin_amdgcn_perm(hi, lo, 0x05040100u);

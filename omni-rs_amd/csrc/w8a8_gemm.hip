@@ -21,7 +21,7 @@
 //    K % 16 == 0). launch_w8a8_mfma picks one with a cost model.
 //  * w8a8_scalar_kernel — v_dot4_i32_i8 per thread, the analog of the
 //    reference's scalar int8_dot; it serves widths that are not a multiple of
-//    16 and the OMNI_INT8_FORCE_SCALAR override.
+//    16 and the OMNI_CONVROT_TENSOROPS=0 / OMNI_INT8_FORCE_SCALAR=1 override.
 #include <atomic>
 #include <cstdlib>
 #include <type_traits>

@@ -98,33 +98,56 @@ def quantize_rows(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Te
     return words.view(torch.int8).reshape(rows, width), scale, total
 
 
+def _vector(t: Optional[torch.Tensor], n: int, dtype: torch.dtype, name: str) -> Optional[torch.Tensor]:
+    """A 1-D operand of n elements of `dtype`, contiguous (a copy if strided).
+    The caller keeps the returned tensor alive until the library call that
+    reads it has returned."""
+    if t is None:
+        return None
+    if t.numel() != n or t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype} [{n}], got {t.dtype} {list(t.shape)}")
+    return t.reshape(-1).contiguous()
+
+
 def w8a8_gemm(codes: torch.Tensor, row_scale: torch.Tensor, row_sum: Optional[torch.Tensor],
               w: torch.Tensor, w_scale: torch.Tensor, w_zero: Optional[torch.Tensor] = None,
               bias: Optional[torch.Tensor] = None, out_dtype: torch.dtype = torch.float32,
               acc_dump: bool = False, lowering: int = OMNI_LOWERING_AUTO):
     """int8 x int8 -> int32 GEMM with the fused reference epilogue
     (int8_matmul.rs:145-373). codes int8 [rows, width]; w int8 [columns, width]
-    (or its packed int32 words); w_scale f32 [columns]; w_zero int32 [columns];
-    bias f32 [columns]. Returns out (and the int32 accumulators if acc_dump)."""
+    (or its packed int32 words); row_scale f32 [rows]; row_sum int32 [rows]
+    (may be None when w_zero is None); w_scale f32 [columns]; w_zero int32
+    [columns]; bias f32 [columns]. Returns out (and the int32 accumulators if
+    acc_dump)."""
     device = _require_gpu(codes, row_scale, row_sum, w, w_scale, w_zero, bias)
+    if codes.dim() != 2 or codes.dtype != torch.int8:
+        raise ValueError("codes must be int8 [rows, width]")
     rows, width = codes.shape
     if w.dtype == torch.int32:
         w = w.view(torch.int8)
+    if w.dtype != torch.int8:
+        raise ValueError("w must be int8 [columns, width] or its int32 words")
     w = w.reshape(-1, width) if w.numel() else w.reshape(0, width)
     columns = w.shape[0]
-    for t, n, dt in ((row_scale, rows, torch.float32), (w_scale, columns, torch.float32)):
-        if t.numel() != n or t.dtype != dt:
-            raise ValueError("scale shape/dtype mismatch")
-    if w_zero is not None and (w_zero.numel() != columns or w_zero.dtype != torch.int32):
-        raise ValueError("w_zero must be int32 [columns]")
-    if bias is not None and (bias.numel() != columns or bias.dtype != torch.float32):
-        raise ValueError("bias must be f32 [columns]")
+    # Every operand the library reads is bound to a local here, so that a
+    # contiguous copy stays allocated until the call has returned (the launch
+    # is stream-ordered; the caching allocator may not hand the block out
+    # again before then).
+    codes_c = codes.contiguous()
+    w_c = w.contiguous()
+    row_scale_c = _vector(row_scale, rows, torch.float32, "row_scale")
+    row_sum_c = _vector(row_sum, rows, torch.int32, "row_sum")
+    w_scale_c = _vector(w_scale, columns, torch.float32, "w_scale")
+    w_zero_c = _vector(w_zero, columns, torch.int32, "w_zero")
+    bias_c = _vector(bias, columns, torch.float32, "bias")
+    if w_zero_c is not None and row_sum_c is None:
+        raise ValueError("row_sum is required when w_zero is given")
     odt = {torch.float32: OMNI_F32, torch.float16: OMNI_F16}[out_dtype]
     out = torch.empty((rows, columns), dtype=out_dtype, device=device)
     acc = torch.empty((rows, columns), dtype=torch.int32, device=device) if acc_dump else None
     st = _lib.check(_lib.lib().omni_w8a8_gemm(
-        _ptr(codes.contiguous()), _ptr(row_scale), _ptr(row_sum), _ptr(w.contiguous()),
-        _ptr(w_scale), _ptr(w_zero), _ptr(bias), rows, columns, width, _ptr(out), odt, _ptr(acc),
+        _ptr(codes_c), _ptr(row_scale_c), _ptr(row_sum_c), _ptr(w_c), _ptr(w_scale_c),
+        _ptr(w_zero_c), _ptr(bias_c), rows, columns, width, _ptr(out), odt, _ptr(acc),
         lowering, _stream(device)))
     if st == OMNI_NOT_HANDLED:
         raise ValueError(_lib.last_error())
@@ -185,12 +208,15 @@ def w8a16_linear(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor,
     columns = w.shape[0]
     if w.shape[1] != width or scale.numel() != columns or (bias is not None and bias.numel() != columns):
         raise ValueError("w8a16_linear: shapes disagree")
+    # contiguous copies bound to locals: alive until the call has returned
     x2 = x2.contiguous()
     w = w.contiguous()
+    scale_c = scale.reshape(-1).contiguous()
+    bias_c = None if bias is None else bias.reshape(-1).contiguous()
     out = torch.empty((x2.shape[0], columns), dtype=torch.float16, device=device)
     st = _lib.check(_lib.lib().omni_w8a16_gemm(
-        _ptr(x2), _ptr(w), _ptr(scale.contiguous()), _ptr(None if bias is None else bias.contiguous()),
-        x2.shape[0], columns, width, _ptr(out), _stream(device)))
+        _ptr(x2), _ptr(w), _ptr(scale_c), _ptr(bias_c), x2.shape[0], columns, width, _ptr(out),
+        _stream(device)))
     if st == OMNI_NOT_HANDLED:
         raise ValueError(_lib.last_error())
     return out.reshape(*lead, columns)
@@ -215,12 +241,15 @@ def w4a16_linear(x: torch.Tensor, w_packed: torch.Tensor, scale: torch.Tensor,
     if (w_packed.shape[-1] * 2 != width or scale.numel() != columns * (width // group)
             or (bias is not None and (bias.dtype != torch.float16 or bias.numel() != columns))):
         raise ValueError("w4a16_linear: shapes disagree")
+    # contiguous copies bound to locals: alive until the call has returned
     x2 = x2.contiguous()
+    w_c = w_packed.contiguous()
+    scale_c = scale.contiguous()
+    bias_c = None if bias is None else bias.reshape(-1).contiguous()
     out = torch.empty((x2.shape[0], columns), dtype=torch.float16, device=device)
     st = _lib.check(_lib.lib().omni_w4a16_gemm(
-        _ptr(x2), _ptr(w_packed.contiguous()), _ptr(scale.contiguous()), group,
-        _ptr(None if bias is None else bias.contiguous()), x2.shape[0], columns, width, _ptr(out),
-        _stream(device)))
+        _ptr(x2), _ptr(w_c), _ptr(scale_c), group, _ptr(bias_c), x2.shape[0], columns, width,
+        _ptr(out), _stream(device)))
     if st == OMNI_NOT_HANDLED:
         raise ValueError(_lib.last_error())
     return out.reshape(*lead, columns)

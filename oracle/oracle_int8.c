@@ -209,6 +209,22 @@ void oracle_int8_gemm(const float* x, int64_t rows, int64_t width, const int8_t*
     free(codes);
 }
 
+/* oracle_int8_gemm with its rows spread over `threads` OpenMP threads: each
+ * row is computed exactly as oracle_int8_gemm computes it (rows are
+ * independent), so the output is bit-identical. It exists to time the
+ * reference's CPU path on every host core as well as on one (the reference
+ * itself is single-threaded, int8_host.rs:19-53). */
+void oracle_int8_gemm_threads(const float* x, int64_t rows, int64_t width, const int8_t* w,
+                              const float* scale, const int32_t* zero, int64_t columns,
+                              float* out, int threads)
+{
+    if (threads < 1)
+        threads = 1;
+#pragma omp parallel for num_threads(threads) schedule(dynamic, 1)
+    for (int64_t r = 0; r < rows; ++r)
+        oracle_int8_gemm(x + r * width, 1, width, w, scale, zero, columns, out + r * columns);
+}
+
 /* Epilogue variant with an optional bias and an fp16 output. The reference op
  * has no bias (crates/qwen-image/src/convrot.rs:30-67 loads none) and returns
  * f32 that its caller casts to the model precision (convrot.rs:89-91). This

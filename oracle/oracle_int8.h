@@ -75,6 +75,11 @@ void oracle_int8_acc(const int8_t* codes, const int8_t* w, int64_t rows, int64_t
 float oracle_epilogue(int32_t acc, int32_t sum, int32_t zero, float row_scale, float w_scale);
 void oracle_int8_gemm(const float* x, int64_t rows, int64_t width, const int8_t* w,
                       const float* scale, const int32_t* zero, int64_t columns, float* out);
+/* The same, rows spread over `threads` OpenMP threads; bit-identical output
+ * (pinned against oracle_int8_gemm in tests/test_oracle.py). */
+void oracle_int8_gemm_threads(const float* x, int64_t rows, int64_t width, const int8_t* w,
+                              const float* scale, const int32_t* zero, int64_t columns,
+                              float* out, int threads);
 void oracle_w8a8_finish(const int32_t* acc, const int32_t* row_sum, const float* row_scale,
                         const float* w_scale, const int32_t* w_zero, const float* bias,
                         int64_t rows, int64_t columns, float* out_f32, uint16_t* out_f16);

@@ -35,6 +35,7 @@ class Oracle:
             "oracle_epilogue": (ctypes.c_float, [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                                  ctypes.c_float, ctypes.c_float]),
             "oracle_int8_gemm": (None, [_P, _I, _I, _P, _P, _P, _I, _P]),
+            "oracle_int8_gemm_threads": (None, [_P, _I, _I, _P, _P, _P, _I, _P, ctypes.c_int]),
             "oracle_w8a8_finish": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _P, _P]),
             "oracle_dequant_reference": (None, [_P, _I, _I, _P, _P, _P, _I, _P]),
             "oracle_w8a16_f64": (None, [_P, _I, _I, _P, _P, _P, _I, _P]),
@@ -113,6 +114,18 @@ class Oracle:
         columns = w.shape[0]
         out = np.empty((rows, columns), dtype=np.float32)
         self.L.oracle_int8_gemm(_p(x), rows, width, _p(w), _p(scale), _p(zero), columns, _p(out))
+        return out
+
+    def int8_gemm_threads(self, x, w, scale, zero, threads):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(w, dtype=np.int8)
+        scale = np.ascontiguousarray(scale, dtype=np.float32)
+        zero = np.ascontiguousarray(zero, dtype=np.int32)
+        rows, width = x.shape
+        columns = w.shape[0]
+        out = np.empty((rows, columns), dtype=np.float32)
+        self.L.oracle_int8_gemm_threads(_p(x), rows, width, _p(w), _p(scale), _p(zero), columns,
+                                        _p(out), int(threads))
         return out
 
     def w8a8_finish(self, acc, row_sum, row_scale, w_scale, w_zero, bias=None):

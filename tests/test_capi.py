@@ -67,11 +67,20 @@ def test_bad_arguments_are_rejected_before_any_launch():
     assert L.omni_w8a16_gemm(None, None, None, None, 1, 4, 24, None, None) == _lib.OMNI_NOT_HANDLED
 
 
-def test_lowering_gate():
+def test_lowering_gate(monkeypatch):
     L = _lib.lib()
-    forced = os.environ.get("OMNI_INT8_FORCE_SCALAR") == "1"
-    assert L.omni_w8a8_lowering(4096) == (_lib.OMNI_LOWERING_SCALAR if forced else _lib.OMNI_LOWERING_MFMA)
+    monkeypatch.delenv("OMNI_INT8_FORCE_SCALAR", raising=False)
+    monkeypatch.delenv("OMNI_CONVROT_TENSOROPS", raising=False)
+    assert L.omni_w8a8_lowering(4096) == _lib.OMNI_LOWERING_MFMA
     assert L.omni_w8a8_lowering(36) == _lib.OMNI_LOWERING_SCALAR
+    # the reference's switch (int8_tensorops.rs:15-20), read on every call
+    monkeypatch.setenv("OMNI_CONVROT_TENSOROPS", "0")
+    assert L.omni_w8a8_lowering(4096) == _lib.OMNI_LOWERING_SCALAR
+    monkeypatch.setenv("OMNI_CONVROT_TENSOROPS", "1")
+    assert L.omni_w8a8_lowering(4096) == _lib.OMNI_LOWERING_MFMA
+    monkeypatch.delenv("OMNI_CONVROT_TENSOROPS")
+    monkeypatch.setenv("OMNI_INT8_FORCE_SCALAR", "1")
+    assert L.omni_w8a8_lowering(4096) == _lib.OMNI_LOWERING_SCALAR
 
 
 def test_device_gate_without_gpu():

@@ -179,6 +179,19 @@ def test_tile64_fixture(oracle):
     assert np.array_equal(got, want)
 
 
+def test_threaded_gemm_is_bit_identical(oracle):
+    # the all-core CPU baseline runs the same per-row computation on threads
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((37, 160)).astype(np.float32)
+    w = rng.integers(-127, 128, (29, 160), dtype=np.int8)
+    scale = rng.uniform(0.002, 0.02, 29).astype(np.float32)
+    zero = rng.integers(-3, 4, 29).astype(np.int32)
+    want = oracle.int8_gemm(x, w, scale, zero)
+    for threads in (1, 3, 8):
+        got = oracle.int8_gemm_threads(x, w, scale, zero, threads)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 def test_finish_f32_equals_gemm_and_f16_is_one_rounding(oracle):
     rng = np.random.default_rng(3)
     x = rng.standard_normal((9, 96)).astype(np.float32)

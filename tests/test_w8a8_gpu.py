@@ -252,10 +252,18 @@ def test_w8a8_every_kernel_variant_f16_bias(oracle, tile, monkeypatch):
 # -- BASELINE configs at full size ---------------------------------------------------
 
 
+def exact_acc(codes, wd):
+    """int32 accumulators of codes @ wd^T through an f64 GEMM on the GPU:
+    every product and partial sum is an integer below 2^53, so f64 is exact."""
+    return (codes.double() @ wd.double().T)
+
+
 def full_size_check(oracle, rows, width, columns, seed, outliers=False, sample_rows=12):
     """Full-size check: the int32 accumulators against an exact f64 GEMM on the
-    GPU (integers below 2^53, so f64 is exact), the f32 epilogue against the
-    reference op order in torch f32, and sampled rows against the C oracle."""
+    GPU, the f32 epilogue against the reference op order in torch f32, and
+    sampled rows against the C oracle. The production build of the kernels
+    (no accumulator dump: the instantiation the bench times) must give the
+    same output bit for bit as the dumping build that is checked."""
     rng = np.random.default_rng(seed)
     x = rng.standard_normal((rows, width)).astype(np.float16)
     if outliers:  # 1% of channels x20 (diffusion config)
@@ -268,11 +276,14 @@ def full_size_check(oracle, rows, width, columns, seed, outliers=False, sample_r
     xd, wd = dev(x), dev(w)
     codes, rs, total = oi.quantize_rows(xd)
     out, acc = oi.w8a8_gemm(codes, rs, total, wd, dev(scale), dev(zero), acc_dump=True)
-    exact = (codes.double() @ wd.double().T)
-    assert torch.equal(acc.double(), exact)
+    assert torch.equal(acc.double(), exact_acc(codes, wd))
     centered = acc - total[:, None] * dev(zero)[None, :]
     ref = (centered.float() * rs[:, None]) * dev(scale)[None, :]
     assert torch.equal(out.view(torch.int32), ref.view(torch.int32))
+    del acc, centered
+    plain = oi.w8a8_gemm(codes, rs, total, wd, dev(scale), dev(zero))
+    assert torch.equal(plain.view(torch.int32), out.view(torch.int32))
+    del plain
     # sampled rows through the C oracle from the f16 input (quantisation included)
     idx = np.unique(np.concatenate([[0, rows - 1], rng.choice(rows, sample_rows, replace=False)]))
     want = oracle.int8_gemm(x[idx].astype(np.float32), w, scale, zero)
@@ -286,6 +297,27 @@ def test_config3_prefill_full_size(oracle, columns):
     full_size_check(oracle, 2048, 4096, columns, seed=columns)
 
 
+@pytest.mark.parametrize("columns", [4096, 14336])
+def test_config3_f16_bias_epilogue_full_size(oracle, columns):
+    # BASELINE config 3 as the bench runs it: zero points absent (w_zero and
+    # row sums NULL), f32 bias, f16 output; every output against the oracle's
+    # epilogue (int8_matmul.rs:156-158 plus the bias add and one RNE cast)
+    # applied to the exact accumulators.
+    rows, width = 2048, 4096
+    rng = np.random.default_rng(31 + columns)
+    x = rng.standard_normal((rows, width)).astype(np.float16)
+    w = rng.integers(-127, 128, (columns, width), dtype=np.int8)
+    scale = rng.uniform(0.002, 0.02, columns).astype(np.float32)
+    bias = rng.standard_normal(columns).astype(np.float32)
+    wd = dev(w)
+    codes, rs, total = oi.quantize_rows(dev(x))
+    out = oi.w8a8_gemm(codes, rs, None, wd, dev(scale), None, dev(bias), torch.float16)
+    acc = exact_acc(codes, wd).to(torch.int32)
+    _, o16 = oracle.w8a8_finish(host(acc), np.zeros(rows, np.int32), host(rs), scale,
+                                np.zeros(columns, np.int32), bias)
+    assert np.array_equal(host(out).view(np.uint16), o16)
+
+
 @pytest.mark.parametrize("width,columns", [(3072, 9216), (3072, 12288), (12288, 3072)])
 def test_config4_diffusion_full_size(oracle, width, columns):
     # M = 4096 + 256 tokens, 1% outlier channels x20
@@ -295,3 +327,95 @@ def test_config4_diffusion_full_size(oracle, width, columns):
 @pytest.mark.parametrize("width,columns", [(3072, 12288), (12288, 3072)])
 def test_north_star_gemm_full_size(oracle, width, columns):
     full_size_check(oracle, 4096, width, columns, seed=7, sample_rows=6)
+
+
+@pytest.mark.parametrize("width,columns", [(3072, 12288), (12288, 3072)])
+def test_north_star_try_int8_gemm_as_benched(oracle, width, columns):
+    # The exact call the bench times: try_int8_gemm on f16 activations with
+    # all-zero zero points, f32 out. Every output against the reference op
+    # order applied to exact accumulators (of the codes the quantiser made,
+    # which the oracle pins below), and sampled rows end to end (quantisation
+    # included) against the C oracle.
+    rows = 4096
+    rng = np.random.default_rng(width ^ columns)
+    x = rng.standard_normal((rows, width)).astype(np.float16)
+    w = rng.integers(-127, 128, (columns, width), dtype=np.int8)
+    scale = rng.uniform(0.002, 0.02, columns).astype(np.float32)
+    zero = np.zeros(columns, np.int32)
+    xd, wd = dev(x), dev(w)
+    out = oi.try_int8_gemm(xd, wd.view(torch.int32).reshape(-1), dev(scale), dev(zero))
+    codes, rs, total = oi.quantize_rows(xd)
+    ref = (exact_acc(codes, wd).to(torch.int32).float() * rs[:, None]) * dev(scale)[None, :]
+    assert torch.equal(out.view(torch.int32), ref.view(torch.int32))
+    idx = np.unique(np.concatenate([[0, rows - 1], rng.choice(rows, 6, replace=False)]))
+    ocodes, _, _ = oracle.quantize_rows(x[idx].astype(np.float32))
+    assert np.array_equal(host(codes)[idx], ocodes)
+    want = oracle.int8_gemm(x[idx].astype(np.float32), w, scale, zero)
+    assert np.array_equal(host(out)[idx].view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,width,columns", [(1, 64, 7), (300, 512, 513), (700, 3072, 650),
+                                                (1000, 4096, 1500)])
+@pytest.mark.parametrize("lowering", [oi.OMNI_LOWERING_MFMA, oi.OMNI_LOWERING_SCALAR])
+def test_w8a8_without_zero_points(oracle, rows, width, columns, lowering):
+    # w_zero and x_sum NULL (the has_zero = false epilogue), f32 and f16+bias.
+    rng = np.random.default_rng(rows * 3 + columns)
+    x = rng.standard_normal((rows, width)).astype(np.float16)
+    w = rng.integers(-128, 128, (columns, width), dtype=np.int8)
+    scale = rng.uniform(0.002, 0.02, columns).astype(np.float32)
+    bias = rng.standard_normal(columns).astype(np.float32)
+    codes, rs, total = oi.quantize_rows(dev(x))
+    out = oi.w8a8_gemm(codes, rs, None, dev(w), dev(scale), None, lowering=lowering)
+    out16 = oi.w8a8_gemm(codes, rs, None, dev(w), dev(scale), None, dev(bias), torch.float16,
+                         lowering=lowering)
+    oacc = oracle.int8_acc(host(codes), w)
+    nz, cz = np.zeros(rows, np.int32), np.zeros(columns, np.int32)
+    o32, _ = oracle.w8a8_finish(oacc, nz, host(rs), scale, cz)
+    _, o16 = oracle.w8a8_finish(oacc, nz, host(rs), scale, cz, bias)
+    assert np.array_equal(host(out).view(np.uint32), o32.view(np.uint32))
+    assert np.array_equal(host(out16).view(np.uint16), o16)
+
+
+def test_w8a8_strided_scales_and_bias(oracle):
+    # 1-D operands given as strided views: the host layer copies them
+    # contiguous and keeps each copy alive until the call has returned, so no
+    # two operands can share a recycled block.
+    rows, width, columns = 300, 1024, 700
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((rows, width)).astype(np.float16)
+    w = rng.integers(-128, 128, (columns, width), dtype=np.int8)
+    scale = rng.uniform(0.002, 0.02, columns).astype(np.float32)
+    zero = rng.integers(-3, 4, columns).astype(np.int32)
+    bias = rng.standard_normal(columns).astype(np.float32)
+    codes, rs, total = oi.quantize_rows(dev(x))
+
+    def strided(a):
+        t = torch.zeros((a.shape[0], 3), dtype=torch.from_numpy(a).dtype, device="cuda")
+        t[:, 1] = dev(a)
+        return t[:, 1]
+
+    rs2 = torch.zeros((rows, 2), device="cuda")
+    rs2[:, 0] = rs
+    tot2 = torch.zeros((rows, 2), dtype=torch.int32, device="cuda")
+    tot2[:, 0] = total
+    s_v, z_v, b_v = strided(scale), strided(zero), strided(bias)
+    assert not s_v.is_contiguous() and not b_v.is_contiguous()
+    for _ in range(3):
+        out = oi.w8a8_gemm(codes, rs2[:, 0], tot2[:, 0], dev(w), s_v, z_v, b_v, torch.float16)
+        oacc = oracle.int8_acc(host(codes), w)
+        _, o16 = oracle.w8a8_finish(oacc, host(total), host(rs), scale, zero, bias)
+        assert np.array_equal(host(out).view(np.uint16), o16)
+
+
+def test_w8a8_rejects_bad_vectors():
+    codes = torch.zeros((4, 64), dtype=torch.int8, device="cuda")
+    w = torch.zeros((8, 64), dtype=torch.int8, device="cuda")
+    rs = torch.ones(4, device="cuda")
+    s = torch.ones(8, device="cuda")
+    z = torch.zeros(8, dtype=torch.int32, device="cuda")
+    with pytest.raises(ValueError):  # row sums of the wrong dtype
+        oi.w8a8_gemm(codes, rs, torch.zeros(4, device="cuda"), w, s, z)
+    with pytest.raises(ValueError):  # row sums of the wrong length
+        oi.w8a8_gemm(codes, rs, torch.zeros(3, dtype=torch.int32, device="cuda"), w, s, z)
+    with pytest.raises(ValueError):  # zero points without row sums
+        oi.w8a8_gemm(codes, rs, None, w, s, z)
