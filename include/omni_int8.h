@@ -119,6 +119,26 @@ int omni_try_int8_gemm(const void* x, int x_dtype, int64_t rows, int64_t width,
                        int64_t scale_len, const int32_t* w_zero, int64_t zero_len, float* out,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of the static device scratch behind omni_try_int8_gemm_noalloc. */
+#define OMNI_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* omni_try_int8_gemm without its workspace argument, for callers that cannot
+ * allocate device memory: code under HIP graph capture that must not call
+ * hipMalloc, tight serving loops, harnesses that forbid allocation. It has
+ * no counterpart in the reference. The codes, row scales and row sums live
+ * in a static device array of OMNI_NOALLOC_SCRATCH_BYTES that each GPU the
+ * library runs on holds until the process ends; shapes whose
+ * omni_try_int8_gemm_workspace_size(rows, width) exceeds it are rejected
+ * with OMNI_BAD_ARGUMENT (64 MiB covers 4352 x 12288 activations). The call
+ * allocates nothing. Every call on one GPU shares that GPU's array: calls
+ * that overlap in time on one GPU (other streams, other host threads) race
+ * on it and must be serialised by the caller. Arguments, guard, result and
+ * NOT_HANDLED convention are omni_try_int8_gemm's. */
+int omni_try_int8_gemm_noalloc(const void* x, int x_dtype, int64_t rows, int64_t width,
+                               const int32_t* w_packed, int64_t w_packed_len, const float* w_scale,
+                               int64_t scale_len, const int32_t* w_zero, int64_t zero_len,
+                               float* out, void* stream);
+
 /* ConvRot activation rotation fused into per-row quantisation.
  * Replaces the rotate step of Int8Linear::forward followed by
  * try_int8_gemm's quantize_rows: crates/qwen-image/src/convrot.rs:86-88 and

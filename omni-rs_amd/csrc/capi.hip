@@ -149,6 +149,67 @@ bool qwen_tensorops_enabled() {
     return value;
 }
 
+// Static device scratch of omni_try_int8_gemm_noalloc: the codes, row scales
+// and row sums that omni_try_int8_gemm keeps in its workspace argument. Each
+// GPU the library runs on holds one copy for the life of the process; calls
+// on one GPU share it, so calls that overlap in time on one GPU (different
+// streams, or host threads) race on it. Nothing in it needs clearing: the
+// quantiser writes every code, scale and sum it later reads.
+constexpr size_t kScratchBytes = OMNI_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+// Per-device address of `scratch`, looked up once per device with that
+// device current. In host code the name `scratch` is a host-side stand-in,
+// never a device address; only the looked-up pointer is passed to kernels.
+uint8_t* g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mutex;
+
+int scratch_of_current_device(uint8_t** out) {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) {
+        (void)hipGetLastError();
+        return fail(OMNI_NO_DEVICE, "try_int8_gemm_noalloc: no usable current device");
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[device]) {
+        void* p = nullptr;
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            (void)hipGetLastError();
+            return fail(OMNI_HIP_ERROR, "try_int8_gemm_noalloc: hipGetSymbolAddress(scratch): %s",
+                        hipGetErrorString(e));
+        }
+        g_scratch_ptr[device] = static_cast<uint8_t*>(p);
+    }
+    *out = g_scratch_ptr[device];
+    return OMNI_OK;
+}
+
+// Shape guard of try_int8_gemm, crates/omni-kernel/src/int8_matmul.rs:517-521,
+// and the argument checks shared by its two entry points.
+int try_int8_gemm_checks(const char* name, const void* x, int x_dtype, int64_t rows,
+                         int64_t width, const int32_t* w_packed, int64_t w_packed_len,
+                         const float* w_scale, int64_t scale_len, const int32_t* w_zero,
+                         int64_t zero_len, float* out) {
+    const int64_t columns = scale_len;
+    if (rows < 0 || width < 0 || columns < 0) return fail(OMNI_BAD_ARGUMENT, "%s: negative size", name);
+    if (width % 4 != 0 || w_packed_len != columns * width / 4 || zero_len != columns)
+        return fail(OMNI_NOT_HANDLED,
+                    "%s: shapes disagree (width=%lld packed=%lld columns=%lld zero=%lld)", name,
+                    (long long)width, (long long)w_packed_len, (long long)columns,
+                    (long long)zero_len);
+    if (x_dtype != OMNI_F32 && x_dtype != OMNI_F16)
+        return fail(OMNI_BAD_ARGUMENT, "%s: unknown dtype %d", name, x_dtype);
+    if (rows == 0 || columns == 0) return OMNI_OK;
+    if (!x || !w_packed || !w_scale || !w_zero || !out)
+        return fail(OMNI_BAD_ARGUMENT, "%s: null pointer", name);
+    return OMNI_OK;
+}
+
+int try_int8_gemm_run(const void* x, int x_dtype, int64_t rows, int64_t width,
+                      const int32_t* w_packed, const float* w_scale, int64_t columns,
+                      const int32_t* w_zero, float* out, uint8_t* ws, void* stream);
+
 }  // namespace
 
 extern "C" {
@@ -218,34 +279,38 @@ int omni_try_int8_gemm(const void* x, int x_dtype, int64_t rows, int64_t width,
                        const int32_t* w_packed, int64_t w_packed_len, const float* w_scale,
                        int64_t scale_len, const int32_t* w_zero, int64_t zero_len, float* out,
                        void* workspace, size_t workspace_bytes, void* stream) {
-    // Shape guard of try_int8_gemm, crates/omni-kernel/src/int8_matmul.rs:517-521.
-    const int64_t columns = scale_len;
-    if (rows < 0 || width < 0 || columns < 0)
-        return fail(OMNI_BAD_ARGUMENT, "try_int8_gemm: negative size");
-    if (width % 4 != 0 || w_packed_len != columns * width / 4 || zero_len != columns)
-        return fail(OMNI_NOT_HANDLED,
-                    "try_int8_gemm: shapes disagree (width=%lld packed=%lld columns=%lld zero=%lld)",
-                    (long long)width, (long long)w_packed_len, (long long)columns,
-                    (long long)zero_len);
-    if (x_dtype != OMNI_F32 && x_dtype != OMNI_F16)
-        return fail(OMNI_BAD_ARGUMENT, "try_int8_gemm: unknown dtype %d", x_dtype);
+    int st = try_int8_gemm_checks("try_int8_gemm", x, x_dtype, rows, width, w_packed, w_packed_len,
+                                  w_scale, scale_len, w_zero, zero_len, out);
+    if (st != OMNI_OK || rows == 0 || scale_len == 0) return st;
     if (workspace_bytes < omni_try_int8_gemm_workspace_size(rows, width))
         return fail(OMNI_BAD_ARGUMENT, "try_int8_gemm: workspace of %zu bytes, need %zu",
                     workspace_bytes, omni_try_int8_gemm_workspace_size(rows, width));
-    if (rows == 0 || columns == 0) return OMNI_OK;
-    if (!x || !w_packed || !w_scale || !w_zero || !out || !workspace)
-        return fail(OMNI_BAD_ARGUMENT, "try_int8_gemm: null pointer");
+    if (!workspace) return fail(OMNI_BAD_ARGUMENT, "try_int8_gemm: null pointer");
     if (!aligned(workspace, 256)) return fail(OMNI_BAD_ARGUMENT, "try_int8_gemm: workspace must be 256-byte aligned");
-    uint8_t* ws = static_cast<uint8_t*>(workspace);
-    int32_t* x_packed = reinterpret_cast<int32_t*>(ws);
-    float* x_scale = reinterpret_cast<float*>(ws + round_up((size_t)rows * width, 256));
-    int32_t* x_sum = reinterpret_cast<int32_t*>(ws + round_up((size_t)rows * width, 256) +
-                                                round_up((size_t)rows * 4, 256));
-    int st = omni_int8_quantize_rows(x, x_dtype, rows, width, width, x_packed, x_scale, x_sum,
-                                     stream);
+    return try_int8_gemm_run(x, x_dtype, rows, width, w_packed, w_scale, scale_len, w_zero, out,
+                             static_cast<uint8_t*>(workspace), stream);
+}
+
+int omni_try_int8_gemm_noalloc(const void* x, int x_dtype, int64_t rows, int64_t width,
+                               const int32_t* w_packed, int64_t w_packed_len, const float* w_scale,
+                               int64_t scale_len, const int32_t* w_zero, int64_t zero_len,
+                               float* out, void* stream) {
+    int st = try_int8_gemm_checks("try_int8_gemm_noalloc", x, x_dtype, rows, width, w_packed,
+                                  w_packed_len, w_scale, scale_len, w_zero, zero_len, out);
+    if (st != OMNI_OK || rows == 0 || scale_len == 0) return st;
+    const size_t need = omni_try_int8_gemm_workspace_size(rows, width);
+    if (need > kScratchBytes)
+        return fail(OMNI_BAD_ARGUMENT,
+                    "try_int8_gemm_noalloc: %lld x %lld activations need %zu bytes of scratch, "
+                    "more than the static %zu (use omni_try_int8_gemm with a workspace)",
+                    (long long)rows, (long long)width, need, kScratchBytes);
+    st = check_current_device();
     if (st != OMNI_OK) return st;
-    return omni_w8a8_gemm(x_packed, x_scale, x_sum, w_packed, w_scale, w_zero, nullptr, rows,
-                          columns, width, out, OMNI_F32, nullptr, OMNI_LOWERING_AUTO, stream);
+    uint8_t* ws = nullptr;
+    st = scratch_of_current_device(&ws);
+    if (st != OMNI_OK) return st;
+    return try_int8_gemm_run(x, x_dtype, rows, width, w_packed, w_scale, scale_len, w_zero, out,
+                             ws, stream);
 }
 
 int omni_convrot_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t width,
@@ -410,3 +475,23 @@ int omni_f16_gemm(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t co
 }
 
 }  // extern "C"
+
+namespace {
+
+// Quantise x into the workspace (codes, then row scales, then row sums, each
+// 256-byte aligned), then the GEMM with the reference's f32 epilogue.
+int try_int8_gemm_run(const void* x, int x_dtype, int64_t rows, int64_t width,
+                      const int32_t* w_packed, const float* w_scale, int64_t columns,
+                      const int32_t* w_zero, float* out, uint8_t* ws, void* stream) {
+    int32_t* x_packed = reinterpret_cast<int32_t*>(ws);
+    float* x_scale = reinterpret_cast<float*>(ws + round_up((size_t)rows * width, 256));
+    int32_t* x_sum = reinterpret_cast<int32_t*>(ws + round_up((size_t)rows * width, 256) +
+                                                round_up((size_t)rows * 4, 256));
+    int st = omni_int8_quantize_rows(x, x_dtype, rows, width, width, x_packed, x_scale, x_sum,
+                                     stream);
+    if (st != OMNI_OK) return st;
+    return omni_w8a8_gemm(x_packed, x_scale, x_sum, w_packed, w_scale, w_zero, nullptr, rows,
+                          columns, width, out, OMNI_F32, nullptr, OMNI_LOWERING_AUTO, stream);
+}
+
+}  // namespace
