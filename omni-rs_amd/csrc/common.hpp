@@ -63,6 +63,46 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
     return v;
 }
 
+// ---- cross-lane moves in registers (no LDS round trip) ----
+
+// DPP move of v within a wave; CTRL is a gfx9 DPP control, every source lane
+// valid for the controls used here.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// The value of lane (lane ^ O) for O in 1, 2, 4, 8: quad_perm for 1 and 2;
+// xor 4 = row_half_mirror (xor 7) after quad_perm [3,2,1,0] (xor 3);
+// xor 8 = row_mirror (xor 15) after row_half_mirror (xor 7).
+template <int O>
+__device__ __forceinline__ float lane_xor(float v) {
+    static_assert(O == 1 || O == 2 || O == 4 || O == 8, "within a row of 16 lanes");
+    if constexpr (O == 1) return dpp_mov<0xB1>(v);                  // quad_perm [1,0,3,2]
+    if constexpr (O == 2) return dpp_mov<0x4E>(v);                  // quad_perm [2,3,0,1]
+    if constexpr (O == 4) return dpp_mov<0x141>(dpp_mov<0x1B>(v));  // half_mirror(quad_perm [3,2,1,0])
+    return dpp_mov<0x140>(dpp_mov<0x141>(v));                       // row_mirror(half_mirror)
+}
+
+// One butterfly step across lanes l and l ^ O for O = 16 or 32 with the
+// gfx950 permlane swaps: lanes with bit O clear return a + a(l ^ O), lanes
+// with it set return b + b(l ^ O). v_permlane16_swap(a, b) returns the rows
+// (16 lanes) {a0, b0, a2, b2} and {a1, b1, a3, b3}; v_permlane32_swap(a, b)
+// the halves {a_lo, b_lo} and {a_hi, b_hi} (lane layout checked on MI355X),
+// so the two results' sum is the step.
+template <int O>
+__device__ __forceinline__ float swap_add(float a, float b) {
+    static_assert(O == 16 || O == 32, "across rows or halves");
+    const unsigned ua = __float_as_uint(a), ub = __float_as_uint(b);
+    if constexpr (O == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(ua, ub, false, false);
+        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(ua, ub, false, false);
+        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+}
+
 // RN(x / s) given y = RN(1 / s): q0 = x * y, r = fma(-q0, s, x),
 // q = fma(r, y, q0) (Markstein's correction step) returns the correctly
 // rounded quotient whenever the residual r is exact, which holds for

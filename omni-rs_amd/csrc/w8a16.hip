@@ -115,8 +115,11 @@ __device__ __forceinline__ void i4x16_dequant(u32 w0, u32 w1, _Float16 s, v2h (&
 
 // Butterfly fold of N partial sums per lane across the 64 lanes of a wave:
 // at each offset O the lanes exchange half of their values, so N values cost
-// about N shuffles instead of 6N. Afterwards every lane holds one complete
-// sum, of index fold_index<N>(lane).
+// about N exchanges instead of 6N. Afterwards every lane holds one complete
+// sum, of index fold_index<N>(lane). Every move stays in registers: offsets
+// 32 and 16 are one permlane swap per pair of values (swap_add), 8 .. 1 are
+// DPP moves (lane_xor), so the fold adds no LDS round trips to the end of
+// the kernel.
 template <int N, int O>
 struct Fold {
     static __device__ __forceinline__ void run(float* v, int lane) {
@@ -124,16 +127,24 @@ struct Fold {
             return;
         } else if constexpr (N > 1) {
             constexpr int H = N / 2;
-            const bool upper = (lane & O) != 0;
+            if constexpr (O >= 16) {
 #pragma unroll
-            for (int i = 0; i < H; ++i) {
-                const float send = upper ? v[i] : v[i + H];
-                const float keep = upper ? v[i + H] : v[i];
-                v[i] = keep + __shfl_xor(send, O, kWave);
+                for (int i = 0; i < H; ++i) v[i] = swap_add<O>(v[i], v[i + H]);
+            } else {
+                const bool upper = (lane & O) != 0;
+#pragma unroll
+                for (int i = 0; i < H; ++i) {
+                    const float send = upper ? v[i] : v[i + H];
+                    const float keep = upper ? v[i + H] : v[i];
+                    v[i] = keep + lane_xor<O>(send);
+                }
             }
             Fold<H, O / 2>::run(v, lane);
         } else {
-            v[0] += __shfl_xor(v[0], O, kWave);
+            if constexpr (O >= 16)
+                v[0] = swap_add<O>(v[0], v[0]);
+            else
+                v[0] += lane_xor<O>(v[0]);
             Fold<1, O / 2>::run(v, lane);
         }
     }
