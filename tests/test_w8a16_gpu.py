@@ -144,6 +144,21 @@ def test_skinny_rows_on_both_routes(oracle, monkeypatch, route, rows, width, col
     assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL, (route, rows, width, columns)
 
 
+@pytest.mark.parametrize("kernel", ["0", "1"])
+@pytest.mark.parametrize("rows,width,columns", [(5, 64, 33), (8, 960, 70), (16, 4096, 4096),
+                                                (13, 2048, 17), (16, 4096, 129), (11, 4032, 300)])
+def test_skinny_lds_kernel_and_fallback(oracle, monkeypatch, kernel, rows, width, columns):
+    # 5..16 rows with K % 64 == 0 and K <= 4096: the LDS-staged skinny kernel
+    # (0) and w8a16_skinny_kernel (OMNI_W8A16_SKINNY=1), with idle waves
+    # (K < 1024), ragged column counts and bias, against the f64 truth.
+    monkeypatch.setenv("OMNI_W8A16_SKINNY", kernel)
+    rng = np.random.default_rng(rows * 5 + width + columns)
+    x, w, s, b = make(rng, rows, width, columns, bias=True)
+    got = host(oi.w8a16_linear(dev(x), dev(w), dev(s), dev(b)))
+    ref = gpu_f64_reference(x, w, s, b)
+    assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL, (kernel, rows, width, columns)
+
+
 @pytest.mark.parametrize("tile", ["1", "2", "4", "5", "6", "7", "8"])
 @pytest.mark.parametrize("rows,width,columns", [(300, 512, 200), (1024, 1536, 1536), (257, 8960, 129),
                                                 (197, 4096, 640), (65, 64, 33), (600, 4096, 700)])
