@@ -147,11 +147,12 @@ int omni_try_int8_gemm_noalloc(const void* x, int x_dtype, int64_t rows, int64_t
  *   r = each group of 256 consecutive elements of a row times H,
  *   H = 2^-4 * H4 (x) H4 (x) H4 (x) H4 with H4[a][b] = -1 iff a ^ b == 3;
  *   then codes, row scales and row sums of r as omni_int8_quantize_rows.
- * r is computed in f32 by a fast transform, not by a 256-term dot: its
- * rounding differs from the reference's f32 matmul by a few ulp, so a code
- * can differ by one where r / row_scale lies within that of k + 0.5. The
- * quotient and the half-add of the rounding are one fused rounding, which
- * moves codes only inside that same band (within 2 ulp of k + 0.5).
+ * r is computed in f32 by a radix-4 fast transform, not by a 256-term dot:
+ * only its rounding differs from the reference's f32 matmul (the error is
+ * at most 12 * 2^-24 * sum|x| over the group, in units of 16 r), so a code can
+ * differ by one where r / row_scale lies within that of k + 0.5. From r on,
+ * the quantisation is omni_int8_quantize_rows' own: the correctly rounded
+ * quotient r / row_scale, then round half away from zero.
  * group must be 256 (convrot.rs:12), width % 256 == 0 (convrot.rs:39-43),
  * else OMNI_NOT_HANDLED; x and every row start (ld_x) 16-byte aligned,
  * x_packed 16-byte aligned. x_sum may be NULL. */

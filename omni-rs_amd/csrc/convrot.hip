@@ -5,8 +5,8 @@
 //   r[row][256 g + c] = sum_j x[row][256 g + j] * H[j][c]          (f32)
 //   H = 2^-4 * (H4 (x) H4 (x) H4 (x) H4),  H4[a][b] = -1 iff a ^ b == 3
 // followed by the per-row quantisation of r as quantize.hip does it (peak,
-// row_scale = max(peak / 127, 1e-30), round half away), with the quotient and
-// the half-add fused into one rounding (row_quot below).
+// row_scale = max(peak / 127, 1e-30), the correctly rounded quotient, round
+// half away; row_quot below).
 // The reference multiplies by the 256 x 256 matrix (an f32 matmul of
 // [rows * K / 256, 256] by H); here the same linear map is applied as four
 // radix-4 stages, one per base-4 digit of the index within the group: the
@@ -142,32 +142,40 @@ __device__ __forceinline__ void rotate_group(const T* g, int sub, float (&v)[4][
     }
 }
 
-// Per-row quotient constants. The rotation is r = u / 16 exactly (a power of
-// two), so the code of r under row scale s is the code of u under 16 s.
-// Codes: c = trunc(RN(u * y + sign(u) / 2)), y = RN(1 / (16 s)): one fused
-// rounding in place of the reference's RN(RN(r / s) + sign / 2). The two
-// differ only where r / s lies within 2 ulp of a half-integer, a band the
-// rotation's own rounding (a few ulp from any 256-term f32 dot) leaves open
-// anyway, and there by one. s >= 1e-30 keeps y = RN(1 / (16 s)) normal.
+// Per-row quotient constants. The kernel holds u = 16 r; the code of r under
+// row scale s is round_half_away(RN(r / s)) (int8_matmul.rs:102-118), and
+// RN(u / (16 s)) is the same quotient: r / s exactly when r is normal, and a
+// code of 0 either way when r is subnormal (|r| < 2^-126, s >= 1e-30).
+// 16 s is exact (s >= 1e-30 is normal). The quotient is div_rn's Markstein
+// step with y = RN(1 / (16 s)), exact for 16 s >= 2^-90; rows below that
+// (tiny) divide with the IEEE division.
 struct RowQuot {
-    float s, y16;
+    float s, s16, y16;
+    bool tiny;
 };
 
 __device__ __forceinline__ RowQuot row_quot(float peak_u) {
     RowQuot q;
     q.s = row_scale_of(peak_u * 0.0625f);   // the peak of r; exact
-    q.y16 = 1.0f / (16.0f * q.s);
+    q.s16 = 16.0f * q.s;
+    q.y16 = 1.0f / q.s16;
+    q.tiny = q.s16 < 0x1p-90f;
     return q;
 }
 
 // Codes of u[0..3], packed little-endian, their sum accumulated, as pack4
-// does. No clamp: |u| <= the row peak, s >= peak / 127 (1 - 2^-23), so
-// |u y| + 1/2 < 127.5001 and the truncation lands in [-127, 127]; NaN gives 0.
-// An infinite u makes the peak, hence s, infinite, and every code 0.
+// does. No clamp: |u| <= the row peak and 16 s >= peak / 127 (1 - 2^-23), so
+// |q| + 1/2 < 127.5001 and the truncation lands in [-127, 127]; NaN gives 0
+// (cvt_i32_sat). An infinite u makes the peak, hence s, infinite, and every
+// code 0.
+template <bool TINY>
 __device__ __forceinline__ u32 pack4_rot(const float* u, const RowQuot& rq, int& sum) {
     int c[4];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) c[b] = cvt_i32_sat(__builtin_fmaf(u[b], rq.y16, __builtin_copysignf(0.5f, u[b])));
+    for (int b = 0; b < 4; ++b) {
+        const float q = div_rn<TINY>(u[b], rq.s16, rq.y16);
+        c[b] = cvt_i32_sat(q + __builtin_copysignf(0.5f, q));
+    }
     const u32 lo = __builtin_amdgcn_perm((u32)c[1], (u32)c[0], 0x0c0c0400u);  // c0.b0, c1.b0
     const u32 hi = __builtin_amdgcn_perm((u32)c[3], (u32)c[2], 0x0c0c0400u);  // c2.b0, c3.b0
     const u32 word = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
@@ -176,14 +184,15 @@ __device__ __forceinline__ u32 pack4_rot(const float* u, const RowQuot& rq, int&
 }
 
 // One lane's 64 codes (4 runs of 16 at out + 64 k) from its rotated values.
+template <bool TINY>
 __device__ __forceinline__ void emit_codes(uint8_t* out, const float (&v)[4][16], const RowQuot& rq, int& sum) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         uint4 w;
-        w.x = pack4_rot(&v[k][0], rq, sum);
-        w.y = pack4_rot(&v[k][4], rq, sum);
-        w.z = pack4_rot(&v[k][8], rq, sum);
-        w.w = pack4_rot(&v[k][12], rq, sum);
+        w.x = pack4_rot<TINY>(&v[k][0], rq, sum);
+        w.y = pack4_rot<TINY>(&v[k][4], rq, sum);
+        w.z = pack4_rot<TINY>(&v[k][8], rq, sum);
+        w.w = pack4_rot<TINY>(&v[k][12], rq, sum);
         *reinterpret_cast<uint4*>(out + 64 * k) = w;
     }
 }
@@ -231,7 +240,16 @@ __global__ __launch_bounds__(256) void convrot_rows_kernel(
     __syncthreads();
     const RowQuot rq = row_quot(__uint_as_float(s_peak[r]));
     int local = 0;
-    if (active) emit_codes(codes + row * width + (int64_t)g * kGroup + 16 * sub, v, rq, local);
+    // Rows of different scales share a wave; the IEEE division runs only in
+    // waves that hold a tiny row (a wave-uniform branch).
+    const bool any_tiny = __builtin_amdgcn_ballot_w64(active && rq.tiny) != 0;
+    if (active) {
+        uint8_t* dst = codes + row * width + (int64_t)g * kGroup + 16 * sub;
+        if (any_tiny)
+            emit_codes<true>(dst, v, rq, local);
+        else
+            emit_codes<false>(dst, v, rq, local);
+    }
     if (sum_out) {
         local += __float_as_int(quad_xor<1>(__int_as_float(local)));
         local += __float_as_int(quad_xor<2>(__int_as_float(local)));
@@ -281,7 +299,13 @@ __global__ __launch_bounds__(256) void convrot_wide_kernel(
     for (int p = 0; p < passes; ++p) {
         const int g = group_of(p);
         rotate_group<T>(g < groups ? src + (int64_t)g * kGroup : src, sub, v);
-        if (g < groups) emit_codes(codes + row * width + (int64_t)g * kGroup + 16 * sub, v, rq, local);
+        if (g < groups) {
+            uint8_t* dst = codes + row * width + (int64_t)g * kGroup + 16 * sub;
+            if (rq.tiny)  // one row per workgroup: uniform
+                emit_codes<true>(dst, v, rq, local);
+            else
+                emit_codes<false>(dst, v, rq, local);
+        }
     }
     if (sum_out) {
         local = wave_sum_i32(local);

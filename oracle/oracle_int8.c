@@ -405,6 +405,103 @@ void oracle_rotate(const float* x, int64_t rows, int64_t width, int64_t group, f
     free(h);
 }
 
+/* The same group-256 rotation as an f32 fast transform, op for op as the GPU
+ * kernel evaluates it (omni-rs_amd/csrc/convrot.hip, rotate_group), so that
+ * the kernel's codes can be checked bit for bit. It returns u = 16 r, the
+ * rotation without its 2^-4 (r = u / 16 is exact for normal values). The
+ * linear map is the reference's H (convrot.rs:121-149) times 16:
+ * H4 (x) H4 (x) H4 (x) H4, H4[a][b] = -1 iff a ^ b == 3, one radix-4 stage per
+ * base-4 digit of the element index within the group, in the order
+ *   digit 0 (index bits 0-1) and digit 1 (bits 2-3), each as
+ *     s = (x0 + x1) + (x2 + x3),  y_a = fma(-2, x_(3-a), s);
+ *   digit 3 (bits 6-7), the same;
+ *   digit 2 (bits 4-5) as y_a = (x_a - x_(a^3)) + (x_(a^1) + x_(a^2)).
+ * Only its rounding differs from the reference's f32 matmul (whose
+ * summation order is its backend's); pinned in tests/test_convrot.py against
+ * the exact rotation (f64) within the transform's error bound and exactly on
+ * unit vectors. */
+static void oracle_h4(float* x0, float* x1, float* x2, float* x3)
+{
+    float s = (*x0 + *x1) + (*x2 + *x3);
+    float y0 = fmaf(-2.0f, *x3, s);
+    float y1 = fmaf(-2.0f, *x2, s);
+    float y2 = fmaf(-2.0f, *x1, s);
+    float y3 = fmaf(-2.0f, *x0, s);
+    *x0 = y0;
+    *x1 = y1;
+    *x2 = y2;
+    *x3 = y3;
+}
+
+void oracle_convrot_fwht(const float* x, int64_t rows, int64_t width, int64_t ld, float* u)
+{
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t g = 0; g + 256 <= width; g += 256) {
+            float v[256];
+            memcpy(v, x + r * ld + g, sizeof v);
+            /* digit 0: elements 4q .. 4q+3 */
+            for (int q = 0; q < 64; ++q)
+                oracle_h4(&v[4 * q], &v[4 * q + 1], &v[4 * q + 2], &v[4 * q + 3]);
+            /* digit 1: within each run of 16, elements e, e+4, e+8, e+12 */
+            for (int b = 0; b < 256; b += 16)
+                for (int e = 0; e < 4; ++e)
+                    oracle_h4(&v[b + e], &v[b + e + 4], &v[b + e + 8], &v[b + e + 12]);
+            /* digit 3: elements i, i+64, i+128, i+192 */
+            for (int i = 0; i < 64; ++i)
+                oracle_h4(&v[i], &v[i + 64], &v[i + 128], &v[i + 192]);
+            /* digit 2: elements i + 16 a for a = 0..3 */
+            for (int k = 0; k < 256; k += 64)
+                for (int e = 0; e < 16; ++e) {
+                    float xa[4], y[4];
+                    for (int a = 0; a < 4; ++a)
+                        xa[a] = v[k + 16 * a + e];
+                    for (int a = 0; a < 4; ++a) {
+                        float d = xa[a] - xa[a ^ 3];
+                        float t = xa[a ^ 1] + xa[a ^ 2];
+                        y[a] = d + t;
+                    }
+                    for (int a = 0; a < 4; ++a)
+                        v[k + 16 * a + e] = y[a];
+                }
+            memcpy(u + r * width + g, v, sizeof v);
+        }
+}
+
+/* ConvRot rotation + quantisation as the GPU kernel computes it: u from
+ * oracle_convrot_fwht, then the per-row quantisation of r = u / 16 of
+ * int8_matmul.rs:23-118 (peak of |r| with NaN skipped, row_scale =
+ * max(peak / 127, 1e-30), code = round_half_away(r / row_scale)), with the
+ * quotient taken as u / (16 row_scale): the same real number whenever r is
+ * normal, and a code of 0 either way when r is subnormal (|r| < 2^-126 and
+ * row_scale >= 1e-30). */
+void oracle_convrot_quantize_fwht(const float* x, int64_t rows, int64_t width, int64_t ld,
+                                  int8_t* codes, float* row_scale, int32_t* row_sum)
+{
+    float* u = (float*)malloc((size_t)width * sizeof(float));
+    for (int64_t r = 0; r < rows; ++r) {
+        oracle_convrot_fwht(x + r * ld, 1, width, width, u);
+        float peak = 0.0f;
+        for (int64_t k = 0; k < width; ++k) {
+            float a = fabsf(u[k]);
+            if (a > peak)
+                peak = a;
+        }
+        float scale = (peak * 0.0625f) / 127.0f;
+        if (!(scale > 1.0e-30f))
+            scale = 1.0e-30f;
+        const float s16 = 16.0f * scale;
+        int32_t sum = 0;
+        for (int64_t k = 0; k < width; ++k) {
+            int32_t c = oracle_round_half_away(u[k] / s16);
+            codes[r * width + k] = (int8_t)c;
+            sum += c;
+        }
+        row_scale[r] = scale;
+        row_sum[r] = sum;
+    }
+    free(u);
+}
+
 /* ---- W4A16 (crates/minicpm-v/src/quant.rs) --------------------------------- */
 
 /* quant.rs:22-29 (unpack_int4): two values per byte, low nibble first, each

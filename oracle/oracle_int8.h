@@ -97,6 +97,14 @@ int oracle_hadamard_sign_negative(uint64_t row, uint64_t column, uint64_t size);
 void oracle_hadamard(int64_t size, float* matrix);
 void oracle_rotate(const float* x, int64_t rows, int64_t width, int64_t group, float* out);
 
+/* The kernel's radix-4 fast transform of each group of 256 (u = 16 r, op for
+ * op as omni-rs_amd/csrc/convrot.hip), and the kernel's codes from it. Pinned
+ * against the exact rotation within the transform's error bound and exactly
+ * on unit vectors (tests/test_convrot.py). */
+void oracle_convrot_fwht(const float* x, int64_t rows, int64_t width, int64_t ld, float* u);
+void oracle_convrot_quantize_fwht(const float* x, int64_t rows, int64_t width, int64_t ld,
+                                  int8_t* codes, float* row_scale, int32_t* row_sum);
+
 void oracle_unpack_int4(const uint8_t* packed, int64_t bytes, int8_t* out);
 float oracle_bf16_to_f32(uint16_t b);
 void oracle_w4a16_dequant(const uint8_t* packed, const uint16_t* scale_bf16, int64_t rows,

@@ -43,6 +43,8 @@ class Oracle:
             "oracle_hadamard_sign_negative": (ctypes.c_int, [ctypes.c_uint64] * 3),
             "oracle_hadamard": (None, [_I, _P]),
             "oracle_rotate": (None, [_P, _I, _I, _I, _P]),
+            "oracle_convrot_fwht": (None, [_P, _I, _I, _I, _P]),
+            "oracle_convrot_quantize_fwht": (None, [_P, _I, _I, _I, _P, _P, _P]),
             "oracle_unpack_int4": (None, [_P, _I, _P]),
             "oracle_bf16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
             "oracle_w4a16_dequant": (None, [_P, _P, _I, _I, _I, ctypes.c_int, _P]),
@@ -191,6 +193,24 @@ class Oracle:
         return out
 
     # -- W4A16 (crates/minicpm-v/src/quant.rs) --------------------------------
+    def convrot_fwht(self, x):
+        """u = 16 r of each group of 256, by the kernel's fast transform."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        rows, width = x.shape
+        u = np.empty((rows, width), dtype=np.float32)
+        self.L.oracle_convrot_fwht(_p(x), rows, width, width, _p(u))
+        return u
+
+    def convrot_quantize_fwht(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        rows, width = x.shape
+        codes = np.empty((rows, width), dtype=np.int8)
+        scale = np.empty(rows, dtype=np.float32)
+        total = np.empty(rows, dtype=np.int32)
+        self.L.oracle_convrot_quantize_fwht(_p(x), rows, width, width, _p(codes), _p(scale),
+                                            _p(total))
+        return codes, scale, total
+
     def unpack_int4(self, packed):
         packed = np.ascontiguousarray(packed, dtype=np.uint8)
         out = np.empty(packed.size * 2, dtype=np.int8)

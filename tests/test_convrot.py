@@ -34,6 +34,67 @@ def test_hadamard_is_the_kronecker_power_of_h4():
     assert np.array_equal(convrot.hadamard(256).astype(np.float64) * 16.0, k)
 
 
+# -- the kernel's fast transform as the oracle restates it -------------------------
+
+
+def test_fast_transform_is_the_hadamard_on_unit_vectors(oracle):
+    # Every op of the transform on a unit vector is exact, so the outputs must
+    # be column j of 16 H exactly: a wrong sign, index or stage order fails.
+    eye = np.eye(256, dtype=np.float32)
+    u = oracle.convrot_fwht(eye)
+    assert np.array_equal(u, convrot.hadamard(256) * np.float32(16.0))
+    # and group by group along a row: group g of a 3-group row sees only its own slice
+    x = np.zeros((256, 768), np.float32)
+    x[:, 256:512] = eye
+    u = oracle.convrot_fwht(x)
+    assert not u[:, :256].any() and not u[:, 512:].any()
+    assert np.array_equal(u[:, 256:512], convrot.hadamard(256) * np.float32(16.0))
+
+
+def _fwht_bound(x):
+    """First-order forward error bound of the four radix-4 stages on u = 16 r:
+    each stage adds at most 3 roundings to every partial sum, whose magnitude
+    is at most the sum of |x| over the inputs feeding it, and the later stages
+    spread an error over disjoint input sets of the group, so the total is
+    12 * 2^-24 * sum_group |x| (plus second-order terms: slack 1 %)."""
+    rows, width = x.shape
+    g = np.abs(x.astype(np.float64)).reshape(rows, width // 256, 256).sum(axis=2)
+    return np.repeat(g, 256, axis=1).reshape(rows, width) * 12.0 * 2.0 ** -24 * 1.01
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_fast_transform_within_its_error_bound_of_the_exact_rotation(oracle, seed):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((64, 3072)).astype(np.float32)
+    x[:, rng.choice(3072, 30, replace=False)] *= 20  # outlier channels
+    x[5] = x[5].astype(np.float16).astype(np.float32)  # f16-valued inputs
+    x[7] *= np.float32(1e-20)  # tiny magnitudes
+    x[9] = np.abs(x[9])  # no cancellation
+    u = oracle.convrot_fwht(x).astype(np.float64)
+    h16 = convrot.hadamard(256).astype(np.float64) * 16.0
+    exact = (x.astype(np.float64).reshape(-1, 256) @ h16).reshape(x.shape)
+    err = np.abs(u - exact)
+    bound = _fwht_bound(x)
+    assert np.all(err <= bound)
+    # the bound is not vacuous: the transform does round
+    assert err.max() > 0
+
+
+def test_fast_transform_codes_follow_the_reference_rule(oracle):
+    # The codes from the fast transform are the reference quantisation of
+    # r = u / 16: checked against quantize_rows on r (which the reference's
+    # own cases pin), bit for bit, including the row scales and sums.
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((40, 1024)).astype(np.float32)
+    x[3] = 0.0
+    x[4] *= np.float32(1e-28)  # row scale at the 1e-30 floor
+    codes, scale, total = oracle.convrot_quantize_fwht(x)
+    r = oracle.convrot_fwht(x) * np.float32(0.0625)
+    rc, rs, rt = oracle.quantize_rows(r)
+    assert np.array_equal(codes, rc) and np.array_equal(total, rt)
+    assert np.array_equal(scale.view(np.uint32), rs.view(np.uint32))
+
+
 def test_rotation_cancels_around_a_float_matmul():
     # convrot.rs:192-220
     h = convrot.hadamard(4)
