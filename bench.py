@@ -106,6 +106,12 @@ def load_traffic():
         return json.load(f)
 
 
+def row_traffic(key):
+    """Measured HBM bytes per launch of one bench row's kernel (None if the
+    row was not profiled); profiles/bench_rows_counters.md lists them."""
+    return load_traffic().get("rows", {}).get(key, {}).get("traffic_bytes")
+
+
 def host_cpu():
     """The host this process runs on: logical CPUs, the CPUs this process may
     use, and the CPU model."""
@@ -278,7 +284,8 @@ def w4a16_bench(torch, oi, gen, dev, stream, steps):
     nbytes = wbytes + 2 * M * K + 2 * M * N
     return {"M": M, "K": K, "N": N, "group": 128, "weight_copies": copies,
             "us_per_launch": round(t * 1e6, 3), "GB/s": round(nbytes / t / 1e9, 1),
-            "roofline_frac": round(nbytes / t / 1e9 / PEAK_HBM_GBS, 4)}
+            "roofline_frac": round(nbytes / t / 1e9 / PEAK_HBM_GBS, 4),
+            "traffic": row_traffic("w4a16_gemv")}
 
 
 def f16_bench(torch, gen, dev, stream, steps):
@@ -308,7 +315,8 @@ def f16_bench(torch, gen, dev, stream, steps):
     nbytes = wbytes + 2 * M * K + 2 * M * N
     res = {"depth_gemv": {"M": M, "K": K, "N": N, "weight_copies": copies,
                           "us_per_launch": round(t * 1e6, 3), "GB/s": round(nbytes / t / 1e9, 1),
-                          "roofline_frac": round(nbytes / t / 1e9 / PEAK_HBM_GBS, 4)}}
+                          "roofline_frac": round(nbytes / t / 1e9 / PEAK_HBM_GBS, 4),
+                          "traffic": row_traffic("f16_depth_gemv")}}
     M, K, N = 4096, 4096, 12288
     x = torch.randn((M, K), generator=gen, device=dev).half()
     w = (torch.randn((N, K), generator=gen, device=dev) * 0.02).half()
@@ -324,7 +332,8 @@ def f16_bench(torch, gen, dev, stream, steps):
     res["dit_gemm"] = {"M": M, "K": K, "N": N, "us": round(times["omni"] * 1e6, 2),
                        "TFLOP/s": round(flops / times["omni"] / 1e12, 1),
                        "roofline_frac": round(flops / times["omni"] / 1e12 / PEAK_F16_TFLOPS, 4),
-                       "torch_matmul_TFLOP/s": round(flops / times["torch_matmul"] / 1e12, 1)}
+                       "torch_matmul_TFLOP/s": round(flops / times["torch_matmul"] / 1e12, 1),
+                       "traffic": row_traffic("f16_dit_gemm")}
     return res
 
 
@@ -351,7 +360,8 @@ def convrot_bench(torch, oi, gen, dev, stream, steps):
         del g
         nbytes = 3 * M * K + 8 * M
         kernels.append({"M": M, "K": K, "us": round(t * 1e6, 2), "GB/s": round(nbytes / t / 1e9, 1),
-                        "roofline_frac": round(nbytes / t / 1e9 / PEAK_HBM_GBS, 4)})
+                        "roofline_frac": round(nbytes / t / 1e9 / PEAK_HBM_GBS, 4),
+                        "traffic": row_traffic(f"convrot_{M}x{K}")})
     res["rotate_quantize"] = kernels
     K, N = 3072, 9216
     x = torch.randn((M, K), generator=gen, device=dev).half()
@@ -416,7 +426,8 @@ def configs_bench(torch, oi, gen, dev, stream, steps):
     nb = N * K + 2 * N + 2 * M * K + 2 * M * N
     res["1_w8a16_m16"] = {"M": M, "K": K, "N": N, "weight_copies": copies,
                           "us": round(t * 1e6, 3), "GB/s": round(nb / t / 1e9, 1),
-                          "roofline_frac": round(nb / t / 1e9 / PEAK_HBM_GBS, 4)}
+                          "roofline_frac": round(nb / t / 1e9 / PEAK_HBM_GBS, 4),
+                          "traffic": row_traffic("w8a16_m16")}
 
     # 2: decode GEMV sweep at 7B shapes, M = 1 and 4.
     sweep = []
@@ -426,9 +437,11 @@ def configs_bench(torch, oi, gen, dev, stream, steps):
             t, copies = rotated_gemv_time(torch, gen, dev, stream, steps, M, K, N, N * K,
                                           w8(N, K), lambda x, w: oi.w8a16_linear(x, w, sc))
             nb = N * K + 2 * N + 2 * M * K + 2 * M * N
+            key = "w8a16_gemv" if (M, K, N) == GEMV_SHAPE else f"gemv_m{M}_{K}x{N}"
             sweep.append({"M": M, "K": K, "N": N, "weight_copies": copies,
                           "us": round(t * 1e6, 3), "GB/s": round(nb / t / 1e9, 1),
-                          "roofline_frac": round(nb / t / 1e9 / PEAK_HBM_GBS, 4)})
+                          "roofline_frac": round(nb / t / 1e9 / PEAK_HBM_GBS, 4),
+                          "traffic": row_traffic(key)})
     res["2_gemv_sweep"] = sweep
 
     def timed(fn, n=steps):
@@ -460,7 +473,8 @@ def configs_bench(torch, oi, gen, dev, stream, steps):
         rows3.append({"M": M, "K": K, "N": N, "out": "f16+bias", "us": round(t * 1e6, 2),
                       "TOPS": round(ops / t / 1e12, 1), "gemm_us": round(tg * 1e6, 2),
                       "gemm_TOPS": round(ops / tg / 1e12, 1),
-                      "gemm_roofline_frac": round(ops / tg / 1e12 / PEAK_INT8_TOPS, 4)})
+                      "gemm_roofline_frac": round(ops / tg / 1e12 / PEAK_INT8_TOPS, 4),
+                      "gemm_traffic": row_traffic(f"w8a8_cfg3_n{N}")})
     res["3_w8a8_prefill"] = rows3
 
     # 4: DiT linears at M=4352 with 1% outlier channels x20, as the production
@@ -479,7 +493,10 @@ def configs_bench(torch, oi, gen, dev, stream, steps):
         t = timed(lambda lin=lin, x=x: lin(x))
         ops = 2.0 * M * N * K
         rows4.append({"layer": name, "M": M, "K": K, "N": N, "out": "f16", "us": round(t * 1e6, 2),
-                      "TOPS": round(ops / t / 1e12, 1)})
+                      "TOPS": round(ops / t / 1e12, 1),
+                      "gemm_traffic": row_traffic("w8a8_cfg4_" + {"qkv": "qkv", "mlp_up": "up",
+                                                                  "mlp_down": "down"}[name]),
+                      "convrot_traffic": row_traffic(f"convrot_{M}x{K}")})
     res["4_dit_convrot_layers"] = rows4
 
     # The floor under every launch: a graph of 400 launches of a 1 x 64 -> 1
@@ -524,6 +541,8 @@ def configs_bench(torch, oi, gen, dev, stream, steps):
     t_dec_f = timed(lambda: run_fused(xd), 16)
     res["5_vlm_mix"] = {
         "layers": L, "hidden": H, "ffn": F, "kv_out": KV, "weight_bytes": wbytes,
+        "prefill_kernel_traffic": {"gate_up": row_traffic("w8a16_cfg5_gateup"),
+                                   "kv": row_traffic("w8a16_cfg5_kv")},
         "prefill_M": 1024, "prefill_ms": round(t_pre * 1e3, 3),
         "prefill_TFLOP/s": round(flops / t_pre / 1e12, 1),
         "decode_step_us": round(t_dec * 1e6, 2), "decode_GB/s": round(dbytes / t_dec / 1e9, 1),
@@ -649,6 +668,7 @@ def main():
         t = times["rotated"]
         gemm_time += t
         per_shape.append({"M": c["M"], "K": c["K"], "N": c["N"], "copies": c["copies"],
+                          "gemm_traffic": row_traffic(f"w8a8_gemm_n{c['N']}"),
                           "gemm_us": round(t * 1e6, 2),
                           "gemm_tops": round(2.0 * c["M"] * c["N"] * c["K"] / t / 1e12, 1),
                           "gemm_us_one_resident_copy": round(times["resident"] * 1e6, 2)})
