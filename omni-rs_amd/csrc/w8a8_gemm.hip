@@ -588,7 +588,21 @@ __global__ __launch_bounds__(128 * WAVES_M, 512 / (128 * WAVES_M)) void w8a8_dma
 // unconditional too: rows and columns past the matrix were loaded clamped to
 // the last row and column, so their values equal the last row's (column's)
 // and are stored there, a duplicate write of the same value.
-template <int BN, int S, bool OUT16, bool DUMP>
+//
+// PAIR = true refills the ring two K tiles at a time. Each copy instruction
+// reads 16 rows x 64 bytes, half of each 128-byte cache line; issued one by
+// one, K tile kt+1's copy of a row comes a full K tile after kt's, by which
+// time the CU has streamed ~56 KB of other lines through its L1 and the line
+// is fetched from L2 a second time. The pair schedule issues copy j of tiles
+// 2p and 2p+1 back to back, so the second half-line read hits the line the
+// first just brought in: L2->L1 traffic halves (measured on MI355X: the K
+// loop's copies cost 12 % instead of 27 % of a 4096x12288x3072 GEMM). With
+// S = 5 slots, pair (t, t+1) goes into slots t%5 and (t+1)%5 once both are
+// free: the first half of its copies after the barrier of tile t-4, the rest
+// in the first half of tile t-3, so tile t is issued at least 2.5 K tiles
+// before it is read. The K loop is unrolled over 2S tiles (slot and pair
+// parity compile-time) with a uniform exit, so any K % 64 == 0 is taken.
+template <int BN, int S, bool OUT16, bool DUMP, bool PAIR = false>
 __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
     constexpr int BM = 256, BK = 64;
     constexpr int WM = 128, WN = BN / 2;
@@ -598,6 +612,13 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
     constexpr int kCpw = kRows / 16 / 4;      // 1 KiB copies per wave per K tile
     static_assert(kRows % 64 == 0 && WN % 32 == 0, "tile shape");
     static_assert(S >= 3 && S <= 5, "3 to 5 stages");
+    static_assert(!PAIR || S == 5, "the pair schedule is laid out for 5 slots");
+    // Pair schedule: copy units (copy j of both tiles of a pair) issued after
+    // the barrier of the refill tile (kPU of them) and in the next tile's
+    // first half (the rest), spread evenly over the MFMAs.
+    constexpr int kPU = (kCpw + 1) / 2, kPU2 = kCpw - kPU;
+    constexpr int kPStep1 = FM * FN / kPU, kPStep2 = kPU2 ? FM * FN / kPU2 : 1;
+    static_assert(!PAIR || (kPStep1 >= 1 && kPStep2 >= 1), "pair units per MFMA group");
     __shared__ __attribute__((aligned(1024))) uint8_t st0[kStage];
     __shared__ __attribute__((aligned(1024))) uint8_t st1[kStage];
     __shared__ __attribute__((aligned(1024))) uint8_t st2[kStage];
@@ -712,14 +733,31 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
         for (int j = 0; j < FN; ++j) fb[j] = *reinterpret_cast<const v4i*>(pb + j * 32 * BK);
     };
 
+    // Copy unit j of the pair (t, t+1): copy j of both tiles, back to back.
+    auto copy_unit = [&](int t, int st, int j) {
+        copy_one(t, st, j);
+        copy_one(t + 1, (st + 1) % S, j);
+    };
+    // The ring's first fill: S tiles, or (pairs) tiles 0..3, slot 4 empty.
+    auto prologue = [&]() {
+        if constexpr (PAIR) {
+#pragma unroll
+            for (int j = 0; j < kCpw; ++j) copy_unit(0, 0, j);
+#pragma unroll
+            for (int j = 0; j < kCpw; ++j) copy_unit(2, 2, j);
+        } else {
+#pragma unroll
+            for (int u = 0; u < S; ++u) copy_tile(u, u);
+        }
+    };
+
     int L = xcd_remap(blockIdx.x, gridDim.x);
     if (L >= total) return;
     tile_origin(L, m0, n0);
     setup_copies();
     load_params(m0, n0);
     store_params(0);
-#pragma unroll
-    for (int u = 0; u < S; ++u) copy_tile(u, u);
+    prologue();
     int parity = 0;
 
     while (true) {
@@ -738,10 +776,54 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
             for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
 
         // Tile 0's copies (and the parameter stores) visible to every wave.
-        s_waitcnt_vm<(S - 1) * kCpw, true>();
+        // Pairs: tile 0's last copy is followed by tile 1's and pair (2, 3).
+        s_waitcnt_vm<PAIR ? 2 * kCpw + 1 : (S - 1) * kCpw, true>();
         lds_barrier();
         read_frags(0, 0, fa0, fb0);
 
+        if constexpr (PAIR) {
+            for (int t0 = 0; t0 < ktiles; t0 += 2 * S) {
+#pragma unroll
+                for (int v = 0; v < 2 * S; ++v) {
+                    const int kt = t0 + v;
+                    if (v > 0 && kt >= ktiles) break;  // uniform
+                    const int u = v % S;               // t0 is a multiple of 2S
+                    // k step 0 | fragment reads of k step 1; odd tiles also
+                    // issue the second part of pair (kt+3, kt+4).
+#pragma unroll
+                    for (int q = 0; q < FM * FN; ++q) {
+                        const int i = q / FN, j = q % FN;
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0[i], fb0[j], acc[i][j], 0, 0, 0);
+                        if (q < FM + FN) read_frag(u, 1, q, fa1, fb1);
+                        if ((v % 2) == 1 && q % kPStep2 == 0 && q / kPStep2 < kPU2)
+                            copy_unit(kt + S - 2, (u + S - 2) % S, kPU + q / kPStep2);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                    // Tile kt+1 landed. Even kt: it ends pair (kt, kt+1),
+                    // followed by all of pair (kt+2, kt+3). Odd kt: it
+                    // starts pair (kt+1, kt+2), followed by that pair's last
+                    // copy and all of pair (kt+3, kt+4).
+                    if ((v % 2) == 0)
+                        s_waitcnt_vm<2 * kCpw, true>();
+                    else
+                        s_waitcnt_vm<2 * kCpw + 1, true>();
+                    lds_barrier();  // slot u is read
+                    // k step 1 | fragment reads of tile kt+1, k step 0; even
+                    // tiles also issue the first part of pair (kt+4, kt+5)
+                    // into slots (kt-1)%S (free since the last barrier but
+                    // one) and u.
+#pragma unroll
+                    for (int q = 0; q < FM * FN; ++q) {
+                        const int i = q / FN, j = q % FN;
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1[i], fb1[j], acc[i][j], 0, 0, 0);
+                        if ((v % 2) == 0 && q % kPStep1 == 0 && q / kPStep1 < kPU)
+                            copy_unit(kt + S - 1, (u + S - 1) % S, q / kPStep1);
+                        if (q < FM + FN) read_frag((u + 1) % S, 0, q, fa0, fb0);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+            }
+        } else
         for (int t0 = 0; t0 < ktiles; t0 += S) {
 #pragma unroll
             for (int u = 0; u < S; ++u) {
@@ -777,15 +859,14 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
         // Every wave is done reading the ring before the next tile's copies
         // (the clamped copies still in flight land first: one wave's loads
         // complete in issue order, and each wave writes its own LDS chunks).
-        s_waitcnt_vm<(S - 1) * kCpw, true>();
+        s_waitcnt_vm<PAIR ? 2 * kCpw : (S - 1) * kCpw, true>();
         lds_barrier();
         if (more) {
             m0 = nm0;
             n0 = nn0;
             setup_copies();
             store_params(parity ^ 1);
-#pragma unroll
-            for (int u = 0; u < S; ++u) copy_tile(u, u);
+            prologue();
         }
 
         // Epilogue. 32x32 accumulator layout: lane holds column (lane & 31)
@@ -917,14 +998,26 @@ bool dma_fits(const W8A8Args& a, int S) {
 template <int BN, int PF>
 hipError_t launch_bn(const W8A8Args& a, hipStream_t stream);
 
-template <int BN, int S, bool OUT16, bool DUMP>
+template <int BN, int S, bool OUT16, bool DUMP, bool PAIR = false>
 hipError_t launch_ring_cfg(const W8A8Args& a, hipStream_t stream) {
     const int64_t tiles = ((a.rows + 255) / 256) * ((a.columns + BN - 1) / BN);
     // Persistent: one workgroup per CU (the kernel's occupancy is one).
     const int64_t grid = tiles < num_cus() ? tiles : num_cus();
-    hipLaunchKernelGGL((w8a8_ring_kernel<BN, S, OUT16, DUMP>), dim3((unsigned)grid), dim3(256), 0,
+    hipLaunchKernelGGL((w8a8_ring_kernel<BN, S, OUT16, DUMP, PAIR>), dim3((unsigned)grid), dim3(256), 0,
                        stream, a);
     return hipGetLastError();
+}
+
+// The pair-refill ring takes any K % 64 == 0.
+template <int BN>
+hipError_t launch_pair(const W8A8Args& a, hipStream_t stream) {
+    if (a.width % 64 != 0 || a.width == 0) return launch_bn<BN == 128 ? 128 : 192, 2>(a, stream);
+    if (a.acc_dump) {
+        if (a.out_f16) return launch_ring_cfg<BN, 5, true, true, true>(a, stream);
+        return launch_ring_cfg<BN, 5, false, true, true>(a, stream);
+    }
+    if (a.out_f16) return launch_ring_cfg<BN, 5, true, false, true>(a, stream);
+    return launch_ring_cfg<BN, 5, false, false, true>(a, stream);
 }
 
 // The ring kernel's K loop takes whole groups of S K tiles of 64 bytes.
@@ -993,18 +1086,23 @@ hipError_t launch_w8a8_mfma(const W8A8Args& a, hipStream_t stream) {
         case 13: return launch_ring<128, 4>(a, stream);
         case 14: return launch_ring<256, 3>(a, stream);
         case 15: return launch_ring<192, 3>(a, stream);
+        case 16: return launch_pair<192>(a, stream);
+        case 17: return launch_pair<128>(a, stream);
         default: break;
     }
     // Cost model, fitted to MI355X timings of every candidate on ten shapes
     // (the BASELINE GEMM shapes and the reference's 256-row benchmark shapes;
-    // random operands, f32 out): a kernel runs its tiles in rounds of one
-    // tile per CU, a round costs BM * BN * (c * K + e) (c: per output element
-    // and K byte; e: the per-tile prologue and epilogue), and a partial last
-    // round with fill f costs (0.7 + 0.3 f) of a full one (the chip is
-    // power-limited on this path, so a partly idle round runs at a higher
-    // clock). It picks the fastest candidate, or one within 1 %, on all ten.
+    // random operands rotated past the MALL, f32 out): a kernel runs its
+    // tiles in rounds of one tile per CU, a round costs BM * BN * (c * K + e)
+    // (c: per output element and K byte; e: the per-tile prologue and
+    // epilogue), and a partial last round with fill f costs (0.7 + 0.3 f) of
+    // a full one (the chip is power-limited on this path, so a partly idle
+    // round runs at a higher clock). It picks the fastest candidate on all
+    // ten, with operands rotated and resident alike; the other kernels
+    // (register-staged, two-waves-per-SIMD DMA, single-refill rings at
+    // 256 x 192 and 256 x 128) lost on every one and stay reachable through
+    // OMNI_W8A8_TILE.
     const int64_t cus = num_cus();
-    const int64_t kt = a.width % 64 == 0 ? a.width / 64 : 0;
     const double K = (double)a.width;
     auto cost = [&](double c, double e, int64_t bm, int64_t bn) {
         const int64_t tiles = ((a.rows + bm - 1) / bm) * ((a.columns + bn - 1) / bn);
@@ -1013,29 +1111,25 @@ hipError_t launch_w8a8_mfma(const W8A8Args& a, hipStream_t stream) {
         return (double)(bm * bn) * (c * K + e) * rounds;
     };
     struct Cand { double t; int id; };
-    Cand best{cost(280.5, 227212.0, 256, 192), 3};  // register-staged 256 x 192 takes any K % 16 == 0
+    if (a.width % 64 != 0) {
+        // Register-staged kernels: any K % 16 == 0.
+        return cost(308.0, 250000.0, 256, 128) < cost(280.5, 227212.0, 256, 192) ? launch_bn<128, 2>(a, stream)
+                                                                                 : launch_bn<192, 2>(a, stream);
+    }
+    const int64_t kt = a.width / 64;
+    Cand best{cost(257.6, 119048.0, 256, 192), 16};
     auto consider = [&](bool ok, double t, int id) {
         if (ok && t < best.t) best = Cand{t, id};
     };
-    consider(true, cost(308.0, 250000.0, 256, 128), 4);
-    consider(dma_fits(a, 2), cost(196.4, 206662.0, 512, 192), 9);
-    consider(dma_fits(a, 2), cost(224.8, 215142.0, 512, 128), 10);
+    consider(true, cost(311.1, 88284.0, 256, 128), 17);
     const bool s4 = kt >= 4 && kt % 4 == 0, s3 = kt >= 3 && kt % 3 == 0;
-    consider(s4, cost(182.2, 278314.0, 256, 256), 11);
-    consider(s4, cost(210.8, 215845.0, 256, 192), 12);
-    consider(s4, cost(262.4, 189679.0, 256, 128), 13);
-    consider(!s4 && s3, cost(208.6, 254981.0, 256, 256), 14);
-    consider(!s4 && s3, cost(233.8, 218505.0, 256, 192), 15);
+    consider(s4, cost(251.9, 182249.0, 256, 256), 11);
+    consider(!s4 && s3, cost(254.6, 196339.0, 256, 256), 14);
     switch (best.id) {
-        case 4: return launch_bn<128, 2>(a, stream);
-        case 9: return launch_dma<192, 2, 4>(a, stream);
-        case 10: return launch_dma<128, 2, 4>(a, stream);
         case 11: return launch_ring<256, 4>(a, stream);
-        case 12: return launch_ring<192, 4>(a, stream);
-        case 13: return launch_ring<128, 4>(a, stream);
         case 14: return launch_ring<256, 3>(a, stream);
-        case 15: return launch_ring<192, 3>(a, stream);
-        default: return launch_bn<192, 2>(a, stream);
+        case 17: return launch_pair<128>(a, stream);
+        default: return launch_pair<192>(a, stream);
     }
 }
 

@@ -209,7 +209,7 @@ def test_w8a8_extreme_codes_no_overflow(oracle):
 # shapes with ragged M/N edges, K tails and multi-round tile grids.
 VARIANT_SHAPES = [(300, 1024, 700), (1000, 4096, 1500), (513, 4160, 389), (700, 3072, 650),
                   (2048, 2048, 3072), (4400, 512, 4100)]
-TILE_VARIANTS = [3, 4, 9, 10, 11, 12, 13, 14, 15]  # OMNI_W8A8_TILE values
+TILE_VARIANTS = [3, 4, 9, 10, 11, 12, 13, 14, 15, 16, 17]  # OMNI_W8A8_TILE values
 
 
 @pytest.mark.parametrize("tile", [0] + TILE_VARIANTS)
@@ -228,6 +228,30 @@ def test_w8a8_every_kernel_variant(oracle, tile, monkeypatch):
         assert torch.equal(acc.double(), exact), (tile, rows, width, columns)
         ref = ((acc - total[:, None] * dev(zero)[None, :]).float() * rs[:, None]) * dev(scale)[None, :]
         assert torch.equal(out.view(torch.int32), ref.view(torch.int32)), (tile, rows, width, columns)
+
+
+@pytest.mark.parametrize("tile", [16, 17])
+def test_w8a8_pair_ring_short_and_odd_k(oracle, tile, monkeypatch):
+    # The pair-refill ring takes any K % 64 == 0: fewer K tiles than the ring
+    # (1, 2, 3, 5), exactly one unrolled pass (10), one more (11), and odd
+    # counts where a pair's second tile is clamped to the last one.
+    monkeypatch.setenv("OMNI_W8A8_TILE", str(tile))
+    for rows, width, columns in [(300, 64, 700), (300, 128, 389), (513, 192, 700), (257, 320, 513),
+                                 (1000, 640, 1500), (600, 704, 400), (520, 1344, 260)]:
+        rng = np.random.default_rng(tile * 1000 + width)
+        x = rng.standard_normal((rows, width)).astype(np.float16)
+        w = rng.integers(-128, 128, (columns, width), dtype=np.int8)
+        scale = rng.uniform(0.002, 0.02, columns).astype(np.float32)
+        zero = rng.integers(-3, 4, columns).astype(np.int32)
+        codes, rs, total = oi.quantize_rows(dev(x))
+        out, acc = oi.w8a8_gemm(codes, rs, total, dev(w), dev(scale), dev(zero), acc_dump=True,
+                                lowering=oi.OMNI_LOWERING_MFMA)
+        exact = codes.double() @ dev(w).double().T
+        assert torch.equal(acc.double(), exact), (tile, rows, width, columns)
+        ref = ((acc - total[:, None] * dev(zero)[None, :]).float() * rs[:, None]) * dev(scale)[None, :]
+        assert torch.equal(out.view(torch.int32), ref.view(torch.int32)), (tile, rows, width, columns)
+        plain = oi.w8a8_gemm(codes, rs, total, dev(w), dev(scale), dev(zero), lowering=oi.OMNI_LOWERING_MFMA)
+        assert torch.equal(plain.view(torch.int32), out.view(torch.int32)), (tile, rows, width, columns)
 
 
 @pytest.mark.parametrize("tile", TILE_VARIANTS)
