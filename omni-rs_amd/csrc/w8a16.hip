@@ -1052,6 +1052,7 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     constexpr int kCpw = kRows / 64;          // 1 KiB copies per wave per K tile
     constexpr int kFrags = 2 * FM + kWH * FN; // fragment reads per pair
     static_assert(kRows % 64 == 0 && FM >= 1 && FN >= 1, "tile shape");
+    static_assert(KP == 1 || kCpw % 2 == 0, "half pairs stay within one wave's copies");
     static_assert(kCpw <= 2 * FM * FN && kFrags <= 2 * FM * FN, "one read and copy per MFMA slot");
     static_assert(S * kStage + 4 * BN * 4 <= 160 * 1024, "LDS");
     __shared__ __attribute__((aligned(1024))) uint8_t st0[kStage];
@@ -1088,13 +1089,33 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
         tm0 = (int64_t)__builtin_amdgcn_readfirstlane(first_m + (l % group_size) % gm) * BM;
         tn0 = (int64_t)__builtin_amdgcn_readfirstlane((l % group_size) / gm) * BN;
     };
+    // The wave's j-th copy fills stage block slot(j) (rows 16 slot .. +15).
+    // On 256-row tiles the issue order pairs the two 64-byte halves of the
+    // same 16 rows (x, and W when it is f16): a wave copies half 0 and then
+    // half 1 of one row block, so the second read finds the 128-byte lines
+    // the first one brought into the CU's L1 (MI355X, 4096 x 4096 x 12288:
+    // 1-4 % faster). Smaller tiles keep block order, in which two waves copy
+    // the two halves side by side (pairing there measured 3-7 % slower on
+    // config 5's M = 1024 shapes).
+    auto slot = [&](int j) -> int {
+        const int g = wave * kCpw + j;  // wave-uniform
+        constexpr int nx = kXR * BM / 16, nw = kWR * BN / 16;
+        if constexpr (KP == 2 && BM >= 256) {
+            if (g < nx) return (g & 1) * (BM / 16) + (g >> 1);
+            if constexpr (WB == 16) {
+                const int gw = g - nx;
+                if (gw < nw) return nx + (gw & 1) * (BN / 16) + (gw >> 1);
+            }
+        }
+        return g;
+    };
     // Copy j reads one matrix (x or W, wave-uniform) at a per-lane 32-bit byte
     // offset from its base (the host keeps both matrices under 4 GiB); the K
     // tile advance is added to the scalar base.
     auto setup_copies = [&]() {
 #pragma unroll
         for (int j = 0; j < kCpw; ++j) {
-            const int c16 = (wave * kCpw + j) * 16;  // wave-uniform
+            const int c16 = slot(j) * 16;  // wave-uniform
             if (c16 < kXR * BM) {
                 const int half = c16 >= BM;
                 const int64_t row = min(m0 + (c16 - half * BM) + cp_row, a.rows - 1);
@@ -1122,10 +1143,11 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     };
     auto copy_one = [&](int kt, int s, int j) {
         const int64_t kk = min(kt, ktiles - 1);
-        const bool is_x = (wave * kCpw + j) * 16 < kXR * BM;  // wave-uniform
+        const int c = slot(j);
+        const bool is_x = c * 16 < kXR * BM;  // wave-uniform
         const uint8_t* base = is_x ? reinterpret_cast<const uint8_t*>(a.x) + kk * 64 * KP
                                    : reinterpret_cast<const uint8_t*>(a.w) + kk * 32 * KP * kWH;
-        lds_copy16_saddr(voff[j], base, stage_lds[s] + (wave * kCpw + j) * 1024);
+        lds_copy16_saddr(voff[j], base, stage_lds[s] + c * 1024);
     };
     auto copy_tile = [&](int kt, int s) {
 #pragma unroll
