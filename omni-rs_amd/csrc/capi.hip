@@ -103,11 +103,11 @@ int run_w8a8(const int32_t* x_packed, const float* x_scale, const int32_t* x_sum
     a.width = width;
     a.out_f16 = out_dtype == OMNI_F16;
     int chosen = lowering == OMNI_LOWERING_AUTO ? omni_w8a8_lowering(width) : lowering;
-    // The MFMA kernel needs 16-byte rows and keeps in-tile output offsets in
-    // 32 bits (256 * columns < 2^31).
+    // The MFMA kernels need 16-byte rows and keep in-tile output offsets in
+    // 32 bits (in bytes: 256 * columns * 4 < 2^32).
     if (chosen == OMNI_LOWERING_MFMA &&
         (width % 16 != 0 || !aligned(x_packed, 16) || !aligned(w_packed, 16) ||
-         columns >= (int64_t(1) << 23)))
+         columns >= (int64_t(1) << 22)))
         chosen = OMNI_LOWERING_SCALAR;
     if (chosen == OMNI_LOWERING_MFMA)
         return hip_status(omni::launch_w8a8_mfma(a, stream), "w8a8 mfma launch");

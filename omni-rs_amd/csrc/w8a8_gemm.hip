@@ -45,6 +45,19 @@ __device__ __forceinline__ float w8a8_epilogue(int acc, int sum, int zero, float
     return v;
 }
 
+// v sign-extended from its low 24 bits (v itself when -2^23 <= v < 2^23):
+// a product of two such values compiles to v_mul_i32_i24 (full rate).
+__device__ __forceinline__ int sext24(int v) { return (int)((unsigned)v << 8) >> 8; }
+
+// The same epilogue on a centred accumulator with the bias always added
+// (a missing bias is -0.0, which leaves every value bit for bit unchanged).
+__device__ __forceinline__ float w8a8_scale(int centered, float row_scale, float w_scale, float bias) {
+#pragma clang fp contract(off)
+    float t = (float)centered * row_scale;
+    float v = t * w_scale;
+    return v + bias;
+}
+
 // Output stores of the MFMA kernels: the output is written once and read by
 // the next operator, not by this kernel, so it is stored nontemporally.
 template <typename T>
@@ -629,6 +642,9 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
     __shared__ float sColScale[2][BN];
     __shared__ int sColZero[2][BN];
     __shared__ float sColBias[2][BN];
+    // Nonzero when a row sum or zero point of the tile lies outside
+    // [-2^23, 2^23): the epilogue then multiplies them in 32 bits.
+    __shared__ int sWide[2];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -650,9 +666,17 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
     // Copy c (0 .. kRows/16) fills stage rows 16c .. 16c+15; this wave owns
     // copies wave*kCpw + j. Lane l reads logical chunk (l%4) ^ ((l/16)%4) of
     // row l/4, landing at physical chunk l%4 (the fragment reads' swizzle).
+    // Copies are inline-assembly LDS-DMA (lds_copy16_saddr): the compiler
+    // sees no LDS write in flight and adds no vmcnt(0) drain of its own
+    // before the ring's LDS reads and writes; the explicit waits below order
+    // every copy. Each reads a wave-uniform base (x or W plus the K tile
+    // offset) plus a 32-bit per-lane byte offset (the host keeps rows * K and
+    // columns * K below 2^32).
     const int cp_row = lane >> 2;
     const int cp_chunk = (lane & 3) ^ ((lane >> 4) & 3);
-    const uint8_t* src[kCpw];
+    unsigned voff[kCpw];
+    const unsigned stage_lds[5] = {lds_addr(st0), lds_addr(st1), lds_addr(st2), S > 3 ? lds_addr(st3) : 0u,
+                                   S > 4 ? lds_addr(st4) : 0u};
     int64_t m0 = 0, n0 = 0;
     float p_rs = 0.0f, p_cs = 0.0f, p_cb = 0.0f;
     int p_rsum = 0, p_cz = 0;
@@ -670,15 +694,17 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
         for (int j = 0; j < kCpw; ++j) {
             const int c16 = (wave * kCpw + j) * 16;  // first stage row of copy j
             const bool is_a = c16 < BM;
-            const uint8_t* base = is_a ? a.x : a.w;
             const int64_t first = is_a ? m0 + c16 : n0 + (c16 - BM);
             const int64_t last = is_a ? a.rows - 1 : a.columns - 1;
             const int64_t row = min(first + cp_row, last);
-            src[j] = base + row * K + cp_chunk * 16;
+            voff[j] = (unsigned)(row * K) + cp_chunk * 16;
         }
     };
     // Epilogue values of the tile at (pm0, pn0) into registers: thread tid
     // holds row tid's and column tid's.
+    // A missing bias is stored as -0.0: v + (-0.0) == v for every v the
+    // epilogue makes (it is never a signalling NaN), so the add is
+    // unconditional and the result is bit-identical to skipping it.
     auto load_params = [&](int64_t pm0, int64_t pn0) {
         const int64_t row = min(pm0 + tid, a.rows - 1);
         p_rs = a.x_scale[row];
@@ -687,9 +713,10 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
             const int64_t col = min(pn0 + tid, a.columns - 1);
             p_cs = a.w_scale[col];
             p_cz = has_zero ? a.w_zero[col] : 0;
-            p_cb = has_bias ? a.bias[col] : 0.0f;
+            p_cb = has_bias ? a.bias[col] : -0.0f;
         }
     };
+    auto fits24 = [](int v) { return (unsigned)v + (1u << 23) < (1u << 24); };
     auto store_params = [&](int p) {
         sRowScale[p][tid] = p_rs;
         sRowSum[p][tid] = p_rsum;
@@ -698,16 +725,17 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
             sColZero[p][tid] = p_cz;
             sColBias[p][tid] = p_cb;
         }
-    };
-    auto copy_tile = [&](int kt, int s) {
-        const int k0 = min(kt, ktiles - 1) * BK;
-        uint8_t* dst = stage(s) + wave * kCpw * 1024;
-#pragma unroll
-        for (int j = 0; j < kCpw; ++j) lds_copy16(src[j] + k0, dst + j * 1024);
+        if (!fits24(p_rsum) || (tid < BN && !fits24(p_cz))) sWide[p] = 1;
     };
     auto copy_one = [&](int kt, int s, int j) {
         const int k0 = min(kt, ktiles - 1) * BK;
-        lds_copy16(src[j] + k0, stage(s) + wave * kCpw * 1024 + j * 1024);
+        const bool is_a = (wave * kCpw + j) * 16 < BM;  // wave-uniform
+        const uint8_t* base = (is_a ? a.x : a.w) + k0;
+        lds_copy16_saddr(voff[j], base, stage_lds[s] + (wave * kCpw + j) * 1024);
+    };
+    auto copy_tile = [&](int kt, int s) {
+#pragma unroll
+        for (int j = 0; j < kCpw; ++j) copy_one(kt, s, j);
     };
 
     // Fragment read offsets within a stage, k steps 0 and 1.
@@ -753,6 +781,8 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
 
     int L = xcd_remap(blockIdx.x, gridDim.x);
     if (L >= total) return;
+    if (tid == 0) sWide[0] = sWide[1] = 0;
+    __syncthreads();
     tile_origin(L, m0, n0);
     setup_copies();
     load_params(m0, n0);
@@ -779,6 +809,10 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
         // Pairs: tile 0's last copy is followed by tile 1's and pair (2, 3).
         s_waitcnt_vm<PAIR ? 2 * kCpw + 1 : (S - 1) * kCpw, true>();
         lds_barrier();
+        // Every wave is past the previous tile's epilogue: its flag may be
+        // cleared for the tile after this one (store_params(parity ^ 1)
+        // comes after this K loop's barriers).
+        if (tid == 0) sWide[parity ^ 1] = 0;
         read_frags(0, 0, fa0, fb0);
 
         if constexpr (PAIR) {
@@ -871,13 +905,18 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
 
         // Epilogue. 32x32 accumulator layout: lane holds column (lane & 31)
         // and rows 8*(r/4) + 4*(lane/32) + (r%4) of each 32x32 block.
-        // Offsets are 32-bit, relative to the tile's first element (the host
-        // guarantees 256 * columns < 2^31).
+        // Stores go to a wave-uniform byte base plus a 32-bit byte offset
+        // (the host guarantees 256 * columns * 4 < 2^32), one add per store.
+        // acc - sum * zero is exact in 24-bit multiplies (full rate) when
+        // every row sum and zero point of the tile lies in [-2^23, 2^23);
+        // otherwise it is formed with 32-bit multiplies (quarter rate).
         const int N = (int)a.columns;
+        constexpr int kES = OUT16 ? 2 : 4;
         const int64_t tile_base = em0 * a.columns + en0;
         int efr = fr, efh = fh;
         asm volatile("" : "+v"(efr), "+v"(efh));
         const bool full = em0 + BM <= a.rows && en0 + BN <= a.columns;
+        const bool wide = __builtin_amdgcn_readfirstlane(sWide[parity]) != 0;
         const int rows_last = (int)min((int64_t)BM, a.rows - em0) - 1;
         const int cols_last = (int)min((int64_t)BN, a.columns - en0) - 1;
         const float* pRowScale = sRowScale[parity];
@@ -885,11 +924,11 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
         const float* pColScale = sColScale[parity];
         const int* pColZero = sColZero[parity];
         const float* pColBias = sColBias[parity];
-        float* out32 = static_cast<float*>(a.out) + tile_base;
-        _Float16* out16 = static_cast<_Float16*>(a.out) + tile_base;
+        char* out_tile = static_cast<char*>(a.out) + tile_base * kES;
         int32_t* dump = DUMP ? a.acc_dump + tile_base : nullptr;
-        auto epilogue = [&](auto clamp_tag) {
+        auto epilogue = [&](auto clamp_tag, auto wide_tag) {
             constexpr bool CLAMP = decltype(clamp_tag)::value;
+            constexpr bool WIDE = decltype(wide_tag)::value;
 #pragma unroll
             for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -899,8 +938,9 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
                     if constexpr (CLAMP) lc = min(lc, cols_last);
                     const float ws = pColScale[lc];
                     const int zero = pColZero[lc];
+                    const int zero24 = sext24(zero);
                     const float bias = pColBias[lc];
-                    const unsigned base = (unsigned)(lr0 * N + lc);
+                    unsigned boff = (unsigned)(lr0 * N + lc) * kES;
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const float4 s4 = *reinterpret_cast<const float4*>(pRowScale + lr0 + 8 * q);
@@ -911,26 +951,38 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
                         for (int e = 0; e < 4; ++e) {
                             unsigned off;
                             if constexpr (CLAMP)
-                                off = (unsigned)(min(lr0 + 8 * q + e, rows_last) * N + lc);
+                                off = (unsigned)(min(lr0 + 8 * q + e, rows_last) * N + lc) * kES;
                             else
-                                off = base + (unsigned)((8 * q + e) * N);
+                                off = boff + (unsigned)((8 * q + e) * N) * kES;
                             const int v = acc[i][j][4 * q + e];
-                            const float o = w8a8_epilogue(v, rsum[e], zero, rs[e], ws, bias, has_bias);
-                            if constexpr (DUMP) dump[off] = v;
+                            // Wrapping int32 arithmetic, as the reference's
+                            // i32 ops; the 24-bit multiply keeps the low 32
+                            // bits of the exact product.
+                            const unsigned prod = WIDE ? (unsigned)rsum[e] * (unsigned)zero
+                                                       : (unsigned)sext24(rsum[e]) * (unsigned)zero24;
+                            const int centered = (int)((unsigned)v - prod);
+                            const float o = w8a8_scale(centered, rs[e], ws, bias);
+                            if constexpr (DUMP) dump[off / kES] = v;
                             if constexpr (OUT16)
-                                stream_store(out16 + off, (_Float16)o);
+                                stream_store(reinterpret_cast<_Float16*>(out_tile + off), (_Float16)o);
                             else
-                                stream_store(out32 + off, o);
+                                stream_store(reinterpret_cast<float*>(out_tile + off), o);
                         }
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
         };
-        if (full)
-            epilogue(std::false_type{});
-        else
-            epilogue(std::true_type{});
+        if (wide) {
+            if (full)
+                epilogue(std::false_type{}, std::true_type{});
+            else
+                epilogue(std::true_type{}, std::true_type{});
+        } else if (full) {
+            epilogue(std::false_type{}, std::false_type{});
+        } else {
+            epilogue(std::true_type{}, std::false_type{});
+        }
         if (!more) break;
         L = Ln;
         parity ^= 1;
@@ -998,6 +1050,13 @@ bool dma_fits(const W8A8Args& a, int S) {
 template <int BN, int PF>
 hipError_t launch_bn(const W8A8Args& a, hipStream_t stream);
 
+// The ring kernels' per-lane copy offsets are 32-bit byte offsets into x
+// and W.
+bool ring_offsets_fit(const W8A8Args& a) {
+    const int64_t lim = int64_t(1) << 32;
+    return a.rows * a.width < lim && a.columns * a.width < lim;
+}
+
 template <int BN, int S, bool OUT16, bool DUMP, bool PAIR = false>
 hipError_t launch_ring_cfg(const W8A8Args& a, hipStream_t stream) {
     const int64_t tiles = ((a.rows + 255) / 256) * ((a.columns + BN - 1) / BN);
@@ -1011,7 +1070,7 @@ hipError_t launch_ring_cfg(const W8A8Args& a, hipStream_t stream) {
 // The pair-refill ring takes any K % 64 == 0.
 template <int BN>
 hipError_t launch_pair(const W8A8Args& a, hipStream_t stream) {
-    if (a.width % 64 != 0 || a.width == 0) return launch_bn<BN == 128 ? 128 : 192, 2>(a, stream);
+    if (a.width % 64 != 0 || a.width == 0 || !ring_offsets_fit(a)) return launch_bn<BN == 128 ? 128 : 192, 2>(a, stream);
     if (a.acc_dump) {
         if (a.out_f16) return launch_ring_cfg<BN, 5, true, true, true>(a, stream);
         return launch_ring_cfg<BN, 5, false, true, true>(a, stream);
@@ -1022,7 +1081,7 @@ hipError_t launch_pair(const W8A8Args& a, hipStream_t stream) {
 
 // The ring kernel's K loop takes whole groups of S K tiles of 64 bytes.
 bool ring_fits(const W8A8Args& a, int S) {
-    return a.width % 64 == 0 && a.width >= 64 * S && (a.width / 64) % S == 0;
+    return a.width % 64 == 0 && a.width >= 64 * S && (a.width / 64) % S == 0 && ring_offsets_fit(a);
 }
 
 template <int BN, int S>
@@ -1111,7 +1170,7 @@ hipError_t launch_w8a8_mfma(const W8A8Args& a, hipStream_t stream) {
         return (double)(bm * bn) * (c * K + e) * rounds;
     };
     struct Cand { double t; int id; };
-    if (a.width % 64 != 0) {
+    if (a.width % 64 != 0 || !ring_offsets_fit(a)) {
         // Register-staged kernels: any K % 16 == 0.
         return cost(308.0, 250000.0, 256, 128) < cost(280.5, 227212.0, 256, 192) ? launch_bn<128, 2>(a, stream)
                                                                                  : launch_bn<192, 2>(a, stream);

@@ -254,6 +254,47 @@ def test_w8a8_pair_ring_short_and_odd_k(oracle, tile, monkeypatch):
         assert torch.equal(plain.view(torch.int32), out.view(torch.int32)), (tile, rows, width, columns)
 
 
+def wrap_i32(t):
+    """int64 tensor -> its value modulo 2^32 as a signed int32 tensor."""
+    return (((t + 2**31) % 2**32) - 2**31).to(torch.int32)
+
+
+@pytest.mark.parametrize("tile", [0] + TILE_VARIANTS)
+def test_w8a8_wide_row_sums_and_zero_points(oracle, tile, monkeypatch):
+    # The epilogue forms acc - row_sum * zero in 24-bit multiplies while every
+    # row sum and zero point of a tile lies in [-2^23, 2^23), and in 32-bit
+    # ones otherwise: caller-supplied sums and zero points at, inside and
+    # outside that range (one wide row or column is enough to switch a whole
+    # tile), with the product wrapping modulo 2^32 as int32 arithmetic does.
+    monkeypatch.setenv("OMNI_W8A8_TILE", str(tile))
+    rows, width, columns = 600, 1024, 520
+    rng = np.random.default_rng(400 + tile)
+    codes = dev(rng.integers(-127, 128, (rows, width), dtype=np.int8))
+    w = dev(rng.integers(-128, 128, (columns, width), dtype=np.int8))
+    rs = dev(rng.uniform(1e-4, 1e-2, rows).astype(np.float32))
+    scale = dev(rng.uniform(0.002, 0.02, columns).astype(np.float32))
+    edge = np.array([2**23 - 1, -2**23, 2**23, -2**23 - 1, 2**31 - 1, -2**31], np.int64)
+    cases = []
+    small_sum = rng.integers(-2**22, 2**22, rows)
+    small_zero = rng.integers(-2**22, 2**22, columns)
+    s1 = small_sum.copy(); s1[:2] = edge[:2]  # boundary values that still fit
+    z1 = small_zero.copy(); z1[:2] = edge[:2]
+    cases.append((s1, z1))
+    s2 = small_sum.copy(); s2[300] = 2**23  # one wide row in the second M tile
+    cases.append((s2, small_zero))
+    z3 = small_zero.copy(); z3[517] = -2**23 - 1  # one wide column in the last N tile
+    cases.append((small_sum, z3))
+    cases.append((rng.integers(-2**31, 2**31, rows), rng.integers(-2**31, 2**31, columns)))
+    acc = (codes.double() @ w.double().T).to(torch.int64)
+    for sums, zeros in cases:
+        total = dev(sums.astype(np.int32))
+        zero = dev(zeros.astype(np.int32))
+        out = oi.w8a8_gemm(codes, rs, total, w, scale, zero, lowering=oi.OMNI_LOWERING_MFMA)
+        centered = wrap_i32(acc - total.long()[:, None] * zero.long()[None, :])
+        ref = (centered.float() * rs[:, None]) * scale[None, :]
+        assert torch.equal(out.view(torch.int32), ref.view(torch.int32)), (tile, int(np.abs(sums).max()))
+
+
 @pytest.mark.parametrize("tile", TILE_VARIANTS)
 def test_w8a8_every_kernel_variant_f16_bias(oracle, tile, monkeypatch):
     # The f16-output and bias epilogue of each variant, on a ragged shape.
