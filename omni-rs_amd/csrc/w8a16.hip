@@ -1037,8 +1037,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a16_mfma_kernel(W
 // there is no scale.
 // KP = 1 (f16 weights only): K tiles of 32 elements, one MFMA pair each, so
 // a stage is half as large and a 256 x 256 tile fits three of them.
-template <int BM, int BN, int WB = 8, int WMW = 2, int S = 3, int KP = 2>
-__global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
+//
+// OCC = 2 (tiles whose ring fits half the LDS): two workgroups share a CU
+// (at most 256 registers per lane each), so one workgroup's prologue and
+// epilogue overlap the other's K loop; the persistent grid is two per CU.
+template <int BM, int BN, int WB = 8, int WMW = 2, int S = 3, int KP = 2, int OCC = 1>
+__global__ __launch_bounds__(256, OCC) void w8a16_ring_kernel(W8A16Args a) {
     static_assert(S == 2 || S == 3, "2 or 3 stages");
     static_assert(KP == 2 || (KP == 1 && WB == 16), "32-element K tiles need f16 weights");
     constexpr int WNW = 4 / WMW;              // waves along N
@@ -1052,9 +1056,8 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     constexpr int kCpw = kRows / 64;          // 1 KiB copies per wave per K tile
     constexpr int kFrags = 2 * FM + kWH * FN; // fragment reads per pair
     static_assert(kRows % 64 == 0 && FM >= 1 && FN >= 1, "tile shape");
-    static_assert(KP == 1 || kCpw % 2 == 0, "half pairs stay within one wave's copies");
     static_assert(kCpw <= 2 * FM * FN && kFrags <= 2 * FM * FN, "one read and copy per MFMA slot");
-    static_assert(S * kStage + 4 * BN * 4 <= 160 * 1024, "LDS");
+    static_assert(S * kStage + 4 * BN * 4 <= 160 * 1024 / OCC, "LDS");
     __shared__ __attribute__((aligned(1024))) uint8_t st0[kStage];
     __shared__ __attribute__((aligned(1024))) uint8_t st1[kStage];
     __shared__ __attribute__((aligned(1024))) uint8_t st2[S > 2 ? kStage : 1024];
@@ -1100,6 +1103,7 @@ __global__ __launch_bounds__(256, 1) void w8a16_ring_kernel(W8A16Args a) {
     auto slot = [&](int j) -> int {
         const int g = wave * kCpw + j;  // wave-uniform
         constexpr int nx = kXR * BM / 16, nw = kWR * BN / 16;
+        // (An odd kCpw lets one pair straddle two waves: still correct.)
         if constexpr (KP == 2 && BM >= 256) {
             if (g < nx) return (g & 1) * (BM / 16) + (g >> 1);
             if constexpr (WB == 16) {
@@ -1354,15 +1358,17 @@ bool ring16_fits(const W8A16Args& a) {
            a.columns < (int64_t(1) << 23);
 }
 
-template <int BM, int BN, int WB = 8, int WMW = 2, int S = 3, int KP = 2>
+template <int BM, int BN, int WB = 8, int WMW = 2, int S = 3, int KP = 2, int OCC = 1>
 hipError_t launch_ring16_cfg(const W8A16Args& a, hipStream_t stream) {
     const int64_t tiles = ((a.rows + BM - 1) / BM) * ((a.columns + BN - 1) / BN);
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         cus = 256;
-    const int64_t grid = tiles < cus ? tiles : cus;
-    hipLaunchKernelGGL((w8a16_ring_kernel<BM, BN, WB, WMW, S, KP>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+    const int64_t slots = (int64_t)cus * OCC;
+    const int64_t grid = tiles < slots ? tiles : slots;
+    hipLaunchKernelGGL((w8a16_ring_kernel<BM, BN, WB, WMW, S, KP, OCC>), dim3((unsigned)grid), dim3(256), 0, stream,
+                       a);
     return hipGetLastError();
 }
 
@@ -1395,8 +1401,10 @@ hipError_t launch_w8a16_skinny(const W8A16Args& a, hipStream_t stream) { return 
 
 // OMNI_W8A16_TILE=<n> pins the prefill GEMM kernel (tuning and test aid):
 // 1 = tiled 128 x 128, 2 = tiled 64 x 64, 4/5/6 = ring 256 x 128 / 128 x 128 /
-// 256 x 256 (2 x 2 waves), 7 = ring 256 x 256 (1 x 4 waves) (rings: K % 64
-// == 0 only). Read on every call.
+// 256 x 256 (2 x 2 waves), 7 = ring 256 x 256 (1 x 4 waves), 8 = ring
+// 64 x 128, 9 = ring 256 x 192, 10 = ring 128 x 128 two workgroups per CU,
+// 11 / 12 = ring 64 x 128 two / three per CU (rings: K % 64 == 0 only).
+// Read on every call.
 int w8a16_tile_override() {
     const char* v = std::getenv("OMNI_W8A16_TILE");
     return v ? std::atoi(v) : 0;
@@ -1413,6 +1421,10 @@ hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream) {
         case 6: if (ring_ok) return launch_ring16_cfg<256, 256>(a, stream); break;
         case 7: if (ring_ok) return launch_ring16_cfg<256, 256, 8, 1>(a, stream); break;
         case 8: if (ring_ok) return launch_ring16_cfg<64, 128>(a, stream); break;
+        case 9: if (ring_ok) return launch_ring16_cfg<256, 192>(a, stream); break;
+        case 10: if (ring_ok) return launch_ring16_cfg<128, 128, 8, 2, 3, 2, 2>(a, stream); break;
+        case 11: if (ring_ok) return launch_ring16_cfg<64, 128, 8, 2, 3, 2, 2>(a, stream); break;
+        case 12: if (ring_ok) return launch_ring16_cfg<64, 128, 8, 2, 3, 2, 3>(a, stream); break;
         default: break;
     }
     // Measured on MI355X (config 5 and the BASELINE GEMM shapes): the ring
@@ -1430,15 +1442,23 @@ hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream) {
     if (ring_ok && a.width >= 3072 && wide_tiles >= cus) return launch_ring16_cfg<256, 256, 8, 1>(a, stream);
     const int64_t ring_tiles = ((a.rows + 255) / 256) * ((a.columns + 127) / 128);
     if (ring_ok && a.width >= 3072 && ring_tiles >= cus) return launch_ring16_cfg<256, 128>(a, stream);
-    // Smaller prefill shapes (config 5's M = 1024 linears, K 1536 and 8960):
-    // the 128 x 128 ring beats the register-staged tiled kernels by 10-35 %;
-    // where even twice its tile count fits in one round of CUs, 64 x 128
-    // tiles keep more CUs busy (1024 x 8960 -> 1536: 54.5 us against 66.8,
-    // 1024 x 1536 -> 1536: 13.4 against 16.6).
+    // Smaller prefill shapes (config 5's M = 1024 linears, K 1536 and 8960),
+    // measured on MI355X against every ring variant:
+    // * 256 x 192 tiles when they fill between half and all of one round of
+    //   CUs on a short K (1024 x 1536 -> 8960: 188 tiles, 43.7 us against
+    //   52.9 for the next best);
+    // * else 64 x 128 tiles three workgroups per CU when they fit in one
+    //   round of those slots (1024 x 8960 -> 1536: 52.4 us against 56.9 at
+    //   one per CU; 1024 x 1536 -> 1536 / 512: 12.7 / 11.8 us against 13.4 /
+    //   12.4);
+    // * else 128 x 128 tiles two per CU (2048 x 4096 -> 4096: 73.6 us
+    //   against 121 for 64 x 128 three per CU).
     if (ring_ok) {
-        const int64_t tiles128 = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
-        if (2 * tiles128 <= cus) return launch_ring16_cfg<64, 128>(a, stream);
-        return launch_ring16_cfg<128, 128>(a, stream);
+        const int64_t tiles192 = ((a.rows + 255) / 256) * ((a.columns + 191) / 192);
+        if (a.width < 3072 && 2 * tiles192 >= cus && tiles192 <= cus) return launch_ring16_cfg<256, 192>(a, stream);
+        const int64_t tiles64 = ((a.rows + 63) / 64) * ((a.columns + 127) / 128);
+        if (tiles64 <= 3 * (int64_t)cus) return launch_ring16_cfg<64, 128, 8, 2, 3, 2, 3>(a, stream);
+        return launch_ring16_cfg<128, 128, 8, 2, 3, 2, 2>(a, stream);
     }
     const int64_t big_tiles = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
     if (big_tiles >= 512) return launch_mfma16_cfg<128, 128, 64, 2, 2, 4>(a, stream);
