@@ -58,6 +58,20 @@ __device__ __forceinline__ float w8a8_scale(int centered, float row_scale, float
     return v + bias;
 }
 
+// Nontemporal stores through a buffer resource (base, 4 GiB range): a
+// per-lane byte offset in a vector register plus a wave-uniform byte offset
+// in a scalar register, so a wave walking rows advances only the scalar part.
+// Cache-policy bit 1 is the nontemporal hint on gfx940 and later.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t out_rsrc(void* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)0xffffffff, 0x00020000);
+}
+__device__ __forceinline__ void buf_store_nt(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, (int)voff, (int)soff, 2);
+}
+__device__ __forceinline__ void buf_store_nt(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff, _Float16 v) {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), r, (int)voff, (int)soff, 2);
+}
+
 // Output stores of the MFMA kernels: the output is written once and read by
 // the next operator, not by this kernel, so it is stored nontemporally.
 template <typename T>
@@ -643,8 +657,10 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
     __shared__ int sColZero[2][BN];
     __shared__ float sColBias[2][BN];
     // Nonzero when a row sum or zero point of the tile lies outside
-    // [-2^23, 2^23): the epilogue then multiplies them in 32 bits.
+    // [-2^23, 2^23) (the epilogue then multiplies them in 32 bits), and when
+    // some zero point of the tile is not 0 (else it drops the sum * zero term).
     __shared__ int sWide[2];
+    __shared__ int sZero[2];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -726,6 +742,7 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
             sColBias[p][tid] = p_cb;
         }
         if (!fits24(p_rsum) || (tid < BN && !fits24(p_cz))) sWide[p] = 1;
+        if (tid < BN && p_cz != 0) sZero[p] = 1;
     };
     auto copy_one = [&](int kt, int s, int j) {
         const int k0 = min(kt, ktiles - 1) * BK;
@@ -781,7 +798,7 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
 
     int L = xcd_remap(blockIdx.x, gridDim.x);
     if (L >= total) return;
-    if (tid == 0) sWide[0] = sWide[1] = 0;
+    if (tid == 0) sWide[0] = sWide[1] = sZero[0] = sZero[1] = 0;
     __syncthreads();
     tile_origin(L, m0, n0);
     setup_copies();
@@ -812,7 +829,7 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
         // Every wave is past the previous tile's epilogue: its flag may be
         // cleared for the tile after this one (store_params(parity ^ 1)
         // comes after this K loop's barriers).
-        if (tid == 0) sWide[parity ^ 1] = 0;
+        if (tid == 0) sWide[parity ^ 1] = sZero[parity ^ 1] = 0;
         read_frags(0, 0, fa0, fb0);
 
         if constexpr (PAIR) {
@@ -905,11 +922,17 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
 
         // Epilogue. 32x32 accumulator layout: lane holds column (lane & 31)
         // and rows 8*(r/4) + 4*(lane/32) + (r%4) of each 32x32 block.
-        // Stores go to a wave-uniform byte base plus a 32-bit byte offset
-        // (the host guarantees 256 * columns * 4 < 2^32), one add per store.
         // acc - sum * zero is exact in 24-bit multiplies (full rate) when
-        // every row sum and zero point of the tile lies in [-2^23, 2^23);
-        // otherwise it is formed with 32-bit multiplies (quarter rate).
+        // every row sum and zero point of the tile lies in [-2^23, 2^23),
+        // otherwise it is formed with 32-bit multiplies (quarter rate), and
+        // it is acc itself when every zero point of the tile is 0. Full tiles
+        // store through a wave-uniform row base (scalar registers) plus one
+        // per-lane byte offset computed once, and take the bias add only when
+        // there is a bias: per element a convert, two multiplies and a store.
+        // Partial tiles (and the accumulator dump) take the general path:
+        // clamped rows and columns, byte offsets from the tile's first
+        // element (the host guarantees 256 * columns * 4 < 2^32), a missing
+        // bias added as -0.0 (which leaves every value bit for bit as it was).
         const int N = (int)a.columns;
         constexpr int kES = OUT16 ? 2 : 4;
         const int64_t tile_base = em0 * a.columns + en0;
@@ -917,6 +940,7 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
         asm volatile("" : "+v"(efr), "+v"(efh));
         const bool full = em0 + BM <= a.rows && en0 + BN <= a.columns;
         const bool wide = __builtin_amdgcn_readfirstlane(sWide[parity]) != 0;
+        const bool zeros = has_zero && __builtin_amdgcn_readfirstlane(sZero[parity]) != 0;
         const int rows_last = (int)min((int64_t)BM, a.rows - em0) - 1;
         const int cols_last = (int)min((int64_t)BN, a.columns - en0) - 1;
         const float* pRowScale = sRowScale[parity];
@@ -926,6 +950,13 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
         const float* pColBias = sColBias[parity];
         char* out_tile = static_cast<char*>(a.out) + tile_base * kES;
         int32_t* dump = DUMP ? a.acc_dump + tile_base : nullptr;
+        auto store_elem = [&](char* p, float o) {
+            if constexpr (OUT16)
+                stream_store(reinterpret_cast<_Float16*>(p), (_Float16)o);
+            else
+                stream_store(reinterpret_cast<float*>(p), o);
+        };
+        // General path: partial tiles and the accumulator dump.
         auto epilogue = [&](auto clamp_tag, auto wide_tag) {
             constexpr bool CLAMP = decltype(clamp_tag)::value;
             constexpr bool WIDE = decltype(wide_tag)::value;
@@ -963,25 +994,88 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
                             const int centered = (int)((unsigned)v - prod);
                             const float o = w8a8_scale(centered, rs[e], ws, bias);
                             if constexpr (DUMP) dump[off / kES] = v;
-                            if constexpr (OUT16)
-                                stream_store(reinterpret_cast<_Float16*>(out_tile + off), (_Float16)o);
-                            else
-                                stream_store(reinterpret_cast<float*>(out_tile + off), o);
+                            store_elem(out_tile + off, o);
                         }
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
         };
-        if (wide) {
-            if (full)
-                epilogue(std::false_type{}, std::true_type{});
+        // Full tiles: ZMODE 0 = no zero-point term, 1 = 24-bit, 2 = 32-bit.
+        auto epilogue_full = [&](auto zmode_tag, auto bias_tag) {
+            constexpr int ZMODE = decltype(zmode_tag)::value;
+            constexpr bool BIAS = decltype(bias_tag)::value;
+            const unsigned lane_off = (unsigned)((4 * efh) * N + wn * WN + efr) * kES;
+            const __amdgpu_buffer_rsrc_t rsrc = out_rsrc(out_tile);
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    const int lc = wn * WN + j * 32 + efr;
+                    const int lr0 = wm * WM + i * 32 + 4 * efh;
+                    const float ws = pColScale[lc];
+                    const int zero = ZMODE ? pColZero[lc] : 0;
+                    const int zero24 = sext24(zero);
+                    const float bias = BIAS ? pColBias[lc] : 0.0f;
+                    // Scalar byte offset of row wm*WM + i*32 + 8q + e of the
+                    // block (the lane's 4*(lane/32) rows are in lane_off),
+                    // advanced by scalar adds; the empty asm keeps the chain
+                    // sequential so 192 offsets are not precomputed and spilled.
+                    unsigned soff = (unsigned)((wm * WM + i * 32) * N + j * 32) * kES;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float4 s4 = *reinterpret_cast<const float4*>(pRowScale + lr0 + 8 * q);
+                        const float rs[4] = {s4.x, s4.y, s4.z, s4.w};
+                        int rsum[4] = {0, 0, 0, 0};
+                        if constexpr (ZMODE != 0) {
+                            const int4 z4 = *reinterpret_cast<const int4*>(pRowSum + lr0 + 8 * q);
+                            rsum[0] = z4.x; rsum[1] = z4.y; rsum[2] = z4.z; rsum[3] = z4.w;
+                        }
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const unsigned so = soff;
+                            soff += (unsigned)(e == 3 ? 5 * N : N) * kES;
+                            asm volatile("" : "+s"(soff));
+                            const int v = acc[i][j][4 * q + e];
+                            int centered = v;
+                            if constexpr (ZMODE == 1)
+                                centered = (int)((unsigned)v - (unsigned)sext24(rsum[e]) * (unsigned)zero24);
+                            else if constexpr (ZMODE == 2)
+                                centered = (int)((unsigned)v - (unsigned)rsum[e] * (unsigned)zero);
+                            float o;
+                            {
+#pragma clang fp contract(off)
+                                const float t = (float)centered * rs[e];
+                                o = t * ws;
+                                if constexpr (BIAS) o = o + bias;
+                            }
+                            if constexpr (OUT16)
+                                buf_store_nt(rsrc, lane_off, so, (_Float16)o);
+                            else
+                                buf_store_nt(rsrc, lane_off, so, o);
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        };
+        auto full_epilogue = [&](auto zmode_tag) {
+            if (has_bias)
+                epilogue_full(zmode_tag, std::true_type{});
             else
+                epilogue_full(zmode_tag, std::false_type{});
+        };
+        if (DUMP || !full) {
+            if (wide)
                 epilogue(std::true_type{}, std::true_type{});
-        } else if (full) {
-            epilogue(std::false_type{}, std::false_type{});
+            else
+                epilogue(std::true_type{}, std::false_type{});
+        } else if (!zeros) {
+            full_epilogue(std::integral_constant<int, 0>{});
+        } else if (!wide) {
+            full_epilogue(std::integral_constant<int, 1>{});
         } else {
-            epilogue(std::true_type{}, std::false_type{});
+            full_epilogue(std::integral_constant<int, 2>{});
         }
         if (!more) break;
         L = Ln;
