@@ -309,9 +309,19 @@ def test_w8a8_every_kernel_variant_f16_bias(oracle, tile, monkeypatch):
     codes, rs, total = oi.quantize_rows(dev(x))
     out = oi.w8a8_gemm(codes, rs, total, dev(w), dev(scale), dev(zero), bias=dev(bias),
                        out_dtype=torch.float16, lowering=oi.OMNI_LOWERING_MFMA)
-    _, o16 = oracle.w8a8_finish(oracle.int8_acc(host(codes), w), host(total), host(rs), scale, zero,
-                                bias)
+    o32, o16 = oracle.w8a8_finish(oracle.int8_acc(host(codes), w), host(total), host(rs), scale, zero,
+                                  bias)
     assert np.array_equal(host(out).view(np.uint16), o16), tile
+    # f32 output with bias, and with all-zero zero points (the epilogue drops
+    # the row-sum term for such tiles)
+    out32 = oi.w8a8_gemm(codes, rs, total, dev(w), dev(scale), dev(zero), bias=dev(bias),
+                         lowering=oi.OMNI_LOWERING_MFMA)
+    assert np.array_equal(host(out32).view(np.uint32), o32.view(np.uint32)), tile
+    z0 = np.zeros(columns, np.int32)
+    out32z = oi.w8a8_gemm(codes, rs, total, dev(w), dev(scale), dev(z0), bias=dev(bias),
+                          lowering=oi.OMNI_LOWERING_MFMA)
+    o32z, _ = oracle.w8a8_finish(oracle.int8_acc(host(codes), w), host(total), host(rs), scale, z0, bias)
+    assert np.array_equal(host(out32z).view(np.uint32), o32z.view(np.uint32)), tile
 
 
 # -- BASELINE configs at full size ---------------------------------------------------
@@ -433,12 +443,14 @@ def test_w8a8_without_zero_points(oracle, rows, width, columns, lowering):
     out = oi.w8a8_gemm(codes, rs, None, dev(w), dev(scale), None, lowering=lowering)
     out16 = oi.w8a8_gemm(codes, rs, None, dev(w), dev(scale), None, dev(bias), torch.float16,
                          lowering=lowering)
+    out32b = oi.w8a8_gemm(codes, rs, None, dev(w), dev(scale), None, dev(bias), lowering=lowering)
     oacc = oracle.int8_acc(host(codes), w)
     nz, cz = np.zeros(rows, np.int32), np.zeros(columns, np.int32)
     o32, _ = oracle.w8a8_finish(oacc, nz, host(rs), scale, cz)
-    _, o16 = oracle.w8a8_finish(oacc, nz, host(rs), scale, cz, bias)
+    o32b, o16 = oracle.w8a8_finish(oacc, nz, host(rs), scale, cz, bias)
     assert np.array_equal(host(out).view(np.uint32), o32.view(np.uint32))
     assert np.array_equal(host(out16).view(np.uint16), o16)
+    assert np.array_equal(host(out32b).view(np.uint32), o32b.view(np.uint32))
 
 
 def test_w8a8_strided_scales_and_bias(oracle):
