@@ -104,6 +104,24 @@ int omni_w8a8_gemm(const int32_t* x_packed, const float* x_scale, const int32_t*
                    const float* bias, int64_t rows, int64_t columns, int64_t width, void* out,
                    int out_dtype, int32_t* acc_dump, int lowering, void* stream);
 
+/* Bytes of workspace omni_w8a8_gemm_ws uses for this shape on the current
+ * device: split-K partial sums (int32 [splits][rows][columns]) for shapes
+ * whose 256 x 128 output tiles alone would leave most CUs idle (the
+ * reference's own 256-row benchmark shapes); 0 when the shape does not
+ * split. */
+size_t omni_w8a8_gemm_workspace_size(int64_t rows, int64_t columns, int64_t width);
+
+/* omni_w8a8_gemm with a caller-owned workspace (256-byte aligned, or NULL
+ * with workspace_bytes 0), which lets the MFMA GEMM split K across
+ * workgroups; with less than omni_w8a8_gemm_workspace_size bytes it splits
+ * less, with none it runs as omni_w8a8_gemm. The int32 partial sums add
+ * exactly, so outputs (and acc_dump) are bit-identical to omni_w8a8_gemm's. */
+int omni_w8a8_gemm_ws(const int32_t* x_packed, const float* x_scale, const int32_t* x_sum,
+                      const int32_t* w_packed, const float* w_scale, const int32_t* w_zero,
+                      const float* bias, int64_t rows, int64_t columns, int64_t width, void* out,
+                      int out_dtype, int32_t* acc_dump, int lowering, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
 /* Workspace bytes omni_try_int8_gemm needs for `rows` x `width` activations
  * (codes, row scales and row sums, each 256-byte aligned). */
 size_t omni_try_int8_gemm_workspace_size(int64_t rows, int64_t width);
@@ -187,6 +205,21 @@ int omni_convrot_linear(const void* x, int x_dtype, int64_t rows, int64_t width,
 int omni_w8a16_gemm(const uint16_t* x, const int8_t* w, const uint16_t* scale,
                     const uint16_t* bias, int64_t rows, int64_t columns, int64_t width,
                     uint16_t* out, void* stream);
+
+/* Bytes of workspace omni_w8a16_gemm_ws uses for this shape on the current
+ * device: split-K partial sums (f32 [splits][rows][columns]) for GEMM shapes
+ * whose output tiles alone would leave CUs idle; 0 when the shape does not
+ * split. */
+size_t omni_w8a16_gemm_workspace_size(int64_t rows, int64_t columns, int64_t width);
+
+/* omni_w8a16_gemm with a caller-owned workspace (256-byte aligned, or NULL
+ * with workspace_bytes 0), which lets the GEMM split K across workgroups;
+ * with less than omni_w8a16_gemm_workspace_size bytes it splits less, with
+ * none it runs as omni_w8a16_gemm. Same contract otherwise (the split sums
+ * K in a different order: f32 rounding differs, not the operation). */
+int omni_w8a16_gemm_ws(const uint16_t* x, const int8_t* w, const uint16_t* scale,
+                       const uint16_t* bias, int64_t rows, int64_t columns, int64_t width,
+                       uint16_t* out, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Weight-only int4 linear (W4A16), the MiniCPM-V pack-quantized format.
  * Replaces the packed-int4 matmul of crates/minicpm-v/src/quant.rs:43-58

@@ -82,12 +82,23 @@ int w8a16_route() {
     return v ? std::atoi(v) : 0;
 }
 
+// The W8A16 route: 0 GEMV, 1 skinny MFMA, 2 the GEMM.
+int w8a16_kind(int64_t rows, int64_t width) {
+    // The GEMV spreads a row over one workgroup of at most 1024 lanes, one
+    // 16-element chunk per lane: width <= 16384.
+    if (rows <= 4 && width <= 16384) return 0;
+    // 5..64 rows: the weights are streamed once by a GEMV-shaped MFMA kernel.
+    if (rows <= 64 && w8a16_route() != 2) return 1;
+    return 2;
+}
+
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 int run_w8a8(const int32_t* x_packed, const float* x_scale, const int32_t* x_sum,
              const int32_t* w_packed, const float* w_scale, const int32_t* w_zero,
              const float* bias, int64_t rows, int64_t columns, int64_t width, void* out,
-             int out_dtype, int32_t* acc_dump, int lowering, hipStream_t stream) {
+             int out_dtype, int32_t* acc_dump, int lowering, hipStream_t stream,
+             int32_t* partial = nullptr, int64_t partial_elems = 0) {
     omni::W8A8Args a;
     a.x = reinterpret_cast<const uint8_t*>(x_packed);
     a.x_scale = x_scale;
@@ -102,6 +113,8 @@ int run_w8a8(const int32_t* x_packed, const float* x_scale, const int32_t* x_sum
     a.columns = columns;
     a.width = width;
     a.out_f16 = out_dtype == OMNI_F16;
+    a.partial = partial;
+    a.partial_elems = partial_elems;
     int chosen = lowering == OMNI_LOWERING_AUTO ? omni_w8a8_lowering(width) : lowering;
     // The MFMA kernels need 16-byte rows and keep in-tile output offsets in
     // 32 bits (in bytes: 256 * columns * 4 < 2^32).
@@ -248,6 +261,24 @@ int omni_w8a8_gemm(const int32_t* x_packed, const float* x_scale, const int32_t*
                    const int32_t* w_packed, const float* w_scale, const int32_t* w_zero,
                    const float* bias, int64_t rows, int64_t columns, int64_t width, void* out,
                    int out_dtype, int32_t* acc_dump, int lowering, void* stream) {
+    return omni_w8a8_gemm_ws(x_packed, x_scale, x_sum, w_packed, w_scale, w_zero, bias, rows, columns, width, out,
+                             out_dtype, acc_dump, lowering, nullptr, 0, stream);
+}
+
+size_t omni_w8a8_gemm_workspace_size(int64_t rows, int64_t columns, int64_t width) {
+    if (rows <= 0 || columns <= 0 || width <= 0 || width % 16 != 0 || width > 131072 ||
+        columns >= (int64_t(1) << 22) || omni_w8a8_lowering(width) != OMNI_LOWERING_MFMA)
+        return 0;
+    return (size_t)omni::w8a8_partial_elems(rows, columns, width) * sizeof(int32_t);
+}
+
+int omni_w8a8_gemm_ws(const int32_t* x_packed, const float* x_scale, const int32_t* x_sum,
+                      const int32_t* w_packed, const float* w_scale, const int32_t* w_zero,
+                      const float* bias, int64_t rows, int64_t columns, int64_t width, void* out,
+                      int out_dtype, int32_t* acc_dump, int lowering, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+    if (workspace_bytes > 0 && (!workspace || !aligned(workspace, 256)))
+        return fail(OMNI_BAD_ARGUMENT, "w8a8_gemm: workspace must be 256-byte aligned");
     if (rows < 0 || columns < 0 || width < 0)
         return fail(OMNI_BAD_ARGUMENT, "w8a8_gemm: negative size");
     if (out_dtype != OMNI_F32 && out_dtype != OMNI_F16)
@@ -266,7 +297,8 @@ int omni_w8a8_gemm(const int32_t* x_packed, const float* x_scale, const int32_t*
     int st = check_current_device();
     if (st != OMNI_OK) return st;
     return run_w8a8(x_packed, x_scale, x_sum, w_packed, w_scale, w_zero, bias, rows, columns,
-                    width, out, out_dtype, acc_dump, lowering, static_cast<hipStream_t>(stream));
+                    width, out, out_dtype, acc_dump, lowering, static_cast<hipStream_t>(stream),
+                    static_cast<int32_t*>(workspace), (int64_t)(workspace_bytes / sizeof(int32_t)));
 }
 
 size_t omni_try_int8_gemm_workspace_size(int64_t rows, int64_t width) {
@@ -385,9 +417,20 @@ int omni_convrot_linear(const void* x, int x_dtype, int64_t rows, int64_t width,
                           columns, width, out, out_dtype, nullptr, OMNI_LOWERING_AUTO, stream);
 }
 
+size_t omni_w8a16_gemm_workspace_size(int64_t rows, int64_t columns, int64_t width) {
+    if (rows <= 0 || columns <= 0 || width <= 0 || width % 16 != 0 || w8a16_kind(rows, width) != 2) return 0;
+    return (size_t)omni::w8a16_partial_elems(rows, columns, width) * sizeof(float);
+}
+
 int omni_w8a16_gemm(const uint16_t* x, const int8_t* w, const uint16_t* scale,
                     const uint16_t* bias, int64_t rows, int64_t columns, int64_t width,
                     uint16_t* out, void* stream) {
+    return omni_w8a16_gemm_ws(x, w, scale, bias, rows, columns, width, out, nullptr, 0, stream);
+}
+
+int omni_w8a16_gemm_ws(const uint16_t* x, const int8_t* w, const uint16_t* scale,
+                       const uint16_t* bias, int64_t rows, int64_t columns, int64_t width,
+                       uint16_t* out, void* workspace, size_t workspace_bytes, void* stream) {
     if (rows < 0 || columns < 0 || width < 0)
         return fail(OMNI_BAD_ARGUMENT, "w8a16_gemm: negative size");
     if (width % 16 != 0) return fail(OMNI_NOT_HANDLED, "w8a16_gemm: width %% 16 != 0");
@@ -395,6 +438,8 @@ int omni_w8a16_gemm(const uint16_t* x, const int8_t* w, const uint16_t* scale,
     if (!x || !w || !scale || !out) return fail(OMNI_BAD_ARGUMENT, "w8a16_gemm: null pointer");
     if (!aligned(x, 16) || !aligned(w, 16))
         return fail(OMNI_BAD_ARGUMENT, "w8a16_gemm: x and w must be 16-byte aligned");
+    if (workspace_bytes > 0 && (!workspace || !aligned(workspace, 256)))
+        return fail(OMNI_BAD_ARGUMENT, "w8a16_gemm: workspace must be 256-byte aligned");
     if (((rows + 63) / 64) * ((columns + 63) / 64) > 0x7fffffffLL)
         return fail(OMNI_BAD_ARGUMENT, "w8a16_gemm: problem too large");
     int st = check_current_device();
@@ -408,15 +453,14 @@ int omni_w8a16_gemm(const uint16_t* x, const int8_t* w, const uint16_t* scale,
     a.rows = rows;
     a.columns = columns;
     a.width = width;
+    a.partial = static_cast<float*>(workspace);
+    a.partial_elems = (int64_t)(workspace_bytes / sizeof(float));
     hipStream_t s = static_cast<hipStream_t>(stream);
-    // The GEMV spreads a row over one workgroup of at most 1024 lanes, one
-    // 16-element chunk per lane: width <= 16384.
-    if (rows <= 4 && width <= 16384)
-        return hip_status(omni::launch_w8a16_gemv(a, s), "w8a16 gemv launch");
-    // 5..64 rows: the weights are streamed once by a GEMV-shaped MFMA kernel.
-    if (rows <= 64 && w8a16_route() != 2)
-        return hip_status(omni::launch_w8a16_skinny(a, s), "w8a16 skinny launch");
-    return hip_status(omni::launch_w8a16_mfma(a, s), "w8a16 mfma launch");
+    switch (w8a16_kind(rows, width)) {
+        case 0: return hip_status(omni::launch_w8a16_gemv(a, s), "w8a16 gemv launch");
+        case 1: return hip_status(omni::launch_w8a16_skinny(a, s), "w8a16 skinny launch");
+        default: return hip_status(omni::launch_w8a16_mfma(a, s), "w8a16 mfma launch");
+    }
 }
 
 int omni_w4a16_gemm(const uint16_t* x, const uint8_t* w_packed, const uint16_t* scale_bf16,

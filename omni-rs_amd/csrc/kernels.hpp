@@ -28,9 +28,14 @@ struct W8A8Args {
     int32_t* acc_dump;     // [rows][columns] or null
     int64_t rows, columns, width;
     bool out_f16;
+    int32_t* partial = nullptr;  // split-K: int32 [splits][rows][columns]
+    int64_t partial_elems = 0;   // int32s available at `partial`
 };
 
 hipError_t launch_w8a8_mfma(const W8A8Args& a, hipStream_t stream);
+// int32s of split-K partial sums launch_w8a8_mfma uses for this shape on the
+// current device (0: no split); with fewer in W8A8Args it splits less.
+int64_t w8a8_partial_elems(int64_t rows, int64_t columns, int64_t width);
 hipError_t launch_w8a8_scalar(const W8A8Args& a, hipStream_t stream);
 
 struct W8A16Args {
@@ -42,11 +47,16 @@ struct W8A16Args {
     int64_t rows, columns, width;
     const uint16_t* gscale = nullptr;  // int4 weights: bf16 [columns][width / group]
     int64_t group = 0;                  // int4 weights: values per scale along K
+    float* partial = nullptr;           // split-K: f32 [splits][rows][columns]
+    int64_t partial_elems = 0;          // floats available at `partial`
 };
 
 hipError_t launch_w8a16_gemv(const W8A16Args& a, hipStream_t stream);
 hipError_t launch_w8a16_skinny(const W8A16Args& a, hipStream_t stream);
 hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream);
+// Floats of split-K partial sums launch_w8a16_mfma uses for this shape on the
+// current device (0: no split); with fewer in W8A16Args it splits less.
+int64_t w8a16_partial_elems(int64_t rows, int64_t columns, int64_t width);
 
 // W4A16 (w8a16.hip): packed int4 weights (two per byte, low nibble first,
 // offset by 8) with bf16 scales per group of K values.

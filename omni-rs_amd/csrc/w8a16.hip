@@ -1041,11 +1041,22 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a16_mfma_kernel(W
 // OCC = 2 (tiles whose ring fits half the LDS): two workgroups share a CU
 // (at most 256 registers per lane each), so one workgroup's prologue and
 // epilogue overlap the other's K loop; the persistent grid is two per CU.
-template <int BM, int BN, int WB = 8, int WMW = 2, int S = 3, int KP = 2, int OCC = 1>
-__global__ __launch_bounds__(256, OCC) void w8a16_ring_kernel(W8A16Args a) {
+//
+// SK (split K, `splits` > 1): the work units are (tile, split) pairs, split s
+// covering K tiles [s * kts, min(ktiles, (s + 1) * kts)) with kts =
+// ceil(ktiles / splits) (the host keeps every split non-empty); a unit stores
+// its unscaled f32 sums to partial[s][rows][columns] and
+// w8a16_split_reduce_kernel adds the splits in order and applies scale and
+// bias. Units of one split are consecutive, so the workgroups of an XCD
+// share that split's K range of x and W.
+//
+// NW = 8: eight waves (two per SIMD) share the ring, each owning half as
+// many accumulators, so one wave's MFMAs can issue while the other waits.
+template <int BM, int BN, int WB = 8, int WMW = 2, int S = 3, int KP = 2, int OCC = 1, bool SK = false, int NW = 4>
+__global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, int splits) {
     static_assert(S == 2 || S == 3, "2 or 3 stages");
     static_assert(KP == 2 || (KP == 1 && WB == 16), "32-element K tiles need f16 weights");
-    constexpr int WNW = 4 / WMW;              // waves along N
+    constexpr int WNW = NW / WMW;             // waves along N
     constexpr int WM = BM / WMW, WN = BN / WNW;
     constexpr int FM = WM / 32, FN = WN / 32;
     constexpr int kWH = WB / 8;               // 64-byte W rows per column per 64 K
@@ -1053,9 +1064,9 @@ __global__ __launch_bounds__(256, OCC) void w8a16_ring_kernel(W8A16Args a) {
     constexpr int kWR = KP == 2 ? kWH : 1;    // 64-byte W rows per column per K tile
     constexpr int kRows = kXR * BM + kWR * BN;  // 64-byte stage rows: x k 0..31 (, x k 32..63), W
     constexpr int kStage = kRows * 64;
-    constexpr int kCpw = kRows / 64;          // 1 KiB copies per wave per K tile
+    constexpr int kCpw = kRows / (16 * NW);   // 1 KiB copies per wave per K tile
     constexpr int kFrags = 2 * FM + kWH * FN; // fragment reads per pair
-    static_assert(kRows % 64 == 0 && FM >= 1 && FN >= 1, "tile shape");
+    static_assert(kRows % (16 * NW) == 0 && FM >= 1 && FN >= 1 && WMW * WNW == NW, "tile shape");
     static_assert(kCpw <= 2 * FM * FN && kFrags <= 2 * FM * FN, "one read and copy per MFMA slot");
     static_assert(S * kStage + 4 * BN * 4 <= 160 * 1024 / OCC, "LDS");
     __shared__ __attribute__((aligned(1024))) uint8_t st0[kStage];
@@ -1071,8 +1082,12 @@ __global__ __launch_bounds__(256, OCC) void w8a16_ring_kernel(W8A16Args a) {
     const int tiles_m = (int)((a.rows + BM - 1) / BM);
     const int tiles_n = (int)((a.columns + BN - 1) / BN);
     const int total = tiles_m * tiles_n;
+    const int units = SK ? total * splits : total;
     const int64_t K = a.width;
-    const int ktiles = (int)(K / (32 * KP));
+    const int ktiles_all = (int)(K / (32 * KP));
+    const int kts = SK ? (ktiles_all + splits - 1) / splits : ktiles_all;
+    // K tiles [kbase, kbase + ktiles) of the unit being copied; split index.
+    int kbase = 0, ktiles = ktiles_all, split = 0;
     const bool has_bias = a.bias != nullptr;
     constexpr int kGroupM = 4;
     auto stage = [&](int s) -> uint8_t* { return s == 0 ? st0 : s == 1 ? st1 : st2; };
@@ -1085,7 +1100,8 @@ __global__ __launch_bounds__(256, OCC) void w8a16_ring_kernel(W8A16Args a) {
     unsigned voff[kCpw];
     int64_t m0 = 0, n0 = 0;
     float p_sc = 0.0f, p_bi = 0.0f;
-    auto tile_origin = [&](int l, int64_t& tm0, int64_t& tn0) {
+    auto tile_origin = [&](int u, int64_t& tm0, int64_t& tn0) {
+        const int l = SK ? u % total : u;
         const int group_size = kGroupM * tiles_n;
         const int first_m = (l / group_size) * kGroupM;
         const int gm = min(tiles_m - first_m, kGroupM);
@@ -1145,8 +1161,15 @@ __global__ __launch_bounds__(256, OCC) void w8a16_ring_kernel(W8A16Args a) {
             sBias[par][tid] = p_bi;
         }
     };
+    auto unit_k = [&](int u) {
+        if constexpr (SK) {
+            split = __builtin_amdgcn_readfirstlane(u / total);
+            kbase = split * kts;
+            ktiles = min(kts, ktiles_all - kbase);
+        }
+    };
     auto copy_one = [&](int kt, int s, int j) {
-        const int64_t kk = min(kt, ktiles - 1);
+        const int64_t kk = kbase + min(kt, ktiles - 1);
         const int c = slot(j);
         const bool is_x = c * 16 < kXR * BM;  // wave-uniform
         const uint8_t* base = is_x ? reinterpret_cast<const uint8_t*>(a.x) + kk * 64 * KP
@@ -1221,8 +1244,9 @@ __global__ __launch_bounds__(256, OCC) void w8a16_ring_kernel(W8A16Args a) {
     };
 
     int L = xcd_remap(blockIdx.x, gridDim.x);
-    if (L >= total) return;
+    if (L >= units) return;
     tile_origin(L, m0, n0);
+    unit_k(L);
     setup_copies();
     load_params(n0);
     store_params(0);
@@ -1232,7 +1256,7 @@ __global__ __launch_bounds__(256, OCC) void w8a16_ring_kernel(W8A16Args a) {
 
     while (true) {
         const int Ln = L + gridDim.x;
-        const bool more = Ln < total;
+        const bool more = Ln < units;
         int64_t nm0 = 0, nn0 = 0;
         if (more) {
             tile_origin(Ln, nm0, nn0);
@@ -1299,11 +1323,13 @@ __global__ __launch_bounds__(256, OCC) void w8a16_ring_kernel(W8A16Args a) {
         }
 
         const int64_t em0 = m0, en0 = n0;
+        const int esplit = split;
         s_waitcnt_vm<(S - 1) * kCpw, true>();
         lds_barrier();  // every wave is done reading the ring
         if (more) {
             m0 = nm0;
             n0 = nn0;
+            unit_k(Ln);
             setup_copies();
             store_params(parity ^ 1);
 #pragma unroll
@@ -1317,7 +1343,30 @@ __global__ __launch_bounds__(256, OCC) void w8a16_ring_kernel(W8A16Args a) {
         // asm so the compiler does not precompute every store address.
         const float* pScale = sScale[parity];
         const float* pBias = sBias[parity];
-        {
+        if constexpr (SK) {
+            // Unscaled f32 sums of this split (plain stores: the reduction
+            // reads them back right after).
+            const int N = (int)a.columns;
+            float* outt = a.partial + (int64_t)esplit * a.rows * a.columns + em0 * a.columns + en0;
+            const int rows_last = (int)min((int64_t)BM, a.rows - em0) - 1;
+            const int cols_last = (int)min((int64_t)BN, a.columns - en0) - 1;
+            int efr = fr, efh = fh;
+            asm volatile("" : "+v"(efr), "+v"(efh));
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    const int lc = wn * WN + j * 32 + efr;
+                    const int lr0 = wm * WM + i * 32 + 4 * efh;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int lr = lr0 + 8 * (r >> 2) + (r & 3);
+                        if (lc <= cols_last && lr <= rows_last) outt[(unsigned)(lr * N + lc)] = acc[i][j][r];
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        } else {
             const int N = (int)a.columns;
             _Float16* outt = a.out + em0 * a.columns + en0;
             const int rows_last = (int)min((int64_t)BM, a.rows - em0) - 1;
@@ -1358,17 +1407,85 @@ bool ring16_fits(const W8A16Args& a) {
            a.columns < (int64_t(1) << 23);
 }
 
-template <int BM, int BN, int WB = 8, int WMW = 2, int S = 3, int KP = 2, int OCC = 1>
-hipError_t launch_ring16_cfg(const W8A16Args& a, hipStream_t stream) {
-    const int64_t tiles = ((a.rows + BM - 1) / BM) * ((a.columns + BN - 1) / BN);
+// Split-K reduction: out[r][c] = f16((sum over s in order of partial[s][r][c])
+// * scale[c] + bias[c]), four consecutive elements per lane.
+__global__ __launch_bounds__(256) void w8a16_split_reduce_kernel(W8A16Args a, int splits) {
+    const int64_t n = a.rows * a.columns;
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= n) return;
+    float v[4];
+    int e_end = 4;
+    if (a.columns % 4 == 0) {
+        float4 s = *reinterpret_cast<const float4*>(a.partial + i);
+        for (int p = 1; p < splits; ++p) {
+            const float4 t = *reinterpret_cast<const float4*>(a.partial + p * n + i);
+            s.x += t.x;
+            s.y += t.y;
+            s.z += t.z;
+            s.w += t.w;
+        }
+        v[0] = s.x, v[1] = s.y, v[2] = s.z, v[3] = s.w;
+    } else {
+        e_end = (int)min((int64_t)4, n - i);
+        for (int e = 0; e < e_end; ++e) {
+            float s = a.partial[i + e];
+            for (int p = 1; p < splits; ++p) s += a.partial[p * n + i + e];
+            v[e] = s;
+        }
+    }
+    int64_t c = i % a.columns;
+    for (int e = 0; e < e_end; ++e) {
+        if (e > 0 && ++c == a.columns) c = 0;
+        const float sc = (float)a.scale[c];
+        const float bi = a.bias ? (float)a.bias[c] : 0.0f;
+        a.out[i + e] = (_Float16)(v[e] * sc + bi);
+    }
+}
+
+int cu_count() {
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         cus = 256;
-    const int64_t slots = (int64_t)cus * OCC;
+    return cus;
+}
+
+// Largest split count <= want that leaves every split of ktiles K tiles
+// non-empty and whose partial sums fit in a.partial_elems floats.
+int fit_splits(const W8A16Args& a, int ktiles, int want) {
+    int s = want < ktiles ? want : ktiles;
+    while (s > 1) {
+        const int kts = (ktiles + s - 1) / s;
+        if ((s - 1) * kts < ktiles && a.partial && s * a.rows * a.columns <= a.partial_elems) break;
+        --s;
+    }
+    return s < 1 ? 1 : s;
+}
+
+template <int BM, int BN, int WB = 8, int WMW = 2, int S = 3, int KP = 2, int OCC = 1, int NW = 4>
+hipError_t launch_ring16_cfg(const W8A16Args& a, hipStream_t stream, int splits = 1) {
+    const int64_t tiles = ((a.rows + BM - 1) / BM) * ((a.columns + BN - 1) / BN);
+    const int64_t slots = (int64_t)cu_count() * OCC;
+    if constexpr (WB == 8) {
+        // Split K when asked for and the partial sums fit (else fewer splits).
+        if (splits > 1) splits = fit_splits(a, (int)(a.width / 64), splits);
+        while (splits > 1 && tiles * splits > INT32_MAX) --splits;  // unit indices are int
+        if (splits > 1) {
+            const int64_t units = tiles * splits;
+            const int64_t grid = units < slots ? units : slots;
+            hipLaunchKernelGGL((w8a16_ring_kernel<BM, BN, WB, WMW, S, KP, OCC, true, NW>), dim3((unsigned)grid),
+                               dim3(64 * NW), 0, stream, a, splits);
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            const int64_t quads = (a.rows * a.columns + 3) / 4;
+            hipLaunchKernelGGL(w8a16_split_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0,
+                               stream, a, splits);
+            return hipGetLastError();
+        }
+    }
     const int64_t grid = tiles < slots ? tiles : slots;
-    hipLaunchKernelGGL((w8a16_ring_kernel<BM, BN, WB, WMW, S, KP, OCC>), dim3((unsigned)grid), dim3(256), 0, stream,
-                       a);
+    hipLaunchKernelGGL((w8a16_ring_kernel<BM, BN, WB, WMW, S, KP, OCC, false, NW>), dim3((unsigned)grid),
+                       dim3(64 * NW), 0, stream, a, 1);
     return hipGetLastError();
 }
 
@@ -1403,66 +1520,111 @@ hipError_t launch_w8a16_skinny(const W8A16Args& a, hipStream_t stream) { return 
 // 1 = tiled 128 x 128, 2 = tiled 64 x 64, 4/5/6 = ring 256 x 128 / 128 x 128 /
 // 256 x 256 (2 x 2 waves), 7 = ring 256 x 256 (1 x 4 waves), 8 = ring
 // 64 x 128, 9 = ring 256 x 192, 10 = ring 128 x 128 two workgroups per CU,
-// 11 / 12 = ring 64 x 128 two / three per CU (rings: K % 64 == 0 only).
+// 11 / 12 = ring 64 x 128 two / three per CU, 16 = ring 128 x 256 with eight
+// waves (rings: K % 64 == 0 only). OMNI_W8A16_SPLITS=<n> adds n-way split K
+// to a pinned ring (or to the shape rule's choice) when the call brings a
+// workspace.
 // Read on every call.
 int w8a16_tile_override() {
     const char* v = std::getenv("OMNI_W8A16_TILE");
     return v ? std::atoi(v) : 0;
 }
 
+// The kernel and split count launch_w8a16_mfma runs for a shape: cfg as
+// OMNI_W8A16_TILE numbers them (0: the register-staged kernels), splits > 1
+// for split K (needs splits * rows * columns floats of partial sums).
+struct W16Plan {
+    int cfg;
+    int splits;
+};
+
+// ws_limited: split only as far as a.partial holds (a launch); else assume
+// the workspace the plan asks for (the size query).
+W16Plan plan_w8a16(const W8A16Args& a, int cus, bool ws_limited) {
+    const char* sv = std::getenv("OMNI_W8A16_SPLITS");
+    const int split_override = sv ? std::atoi(sv) : 0;
+    const bool ring_ok = ring16_fits(a);
+    const int ov = w8a16_tile_override();
+    if (ov == 1 || ov == 2 || (ov >= 4 && ov <= 12 && ring_ok) || (ov == 16 && ring_ok))
+        return {ov, ov >= 4 && split_override > 1 ? split_override : 1};
+    if (!ring_ok) {
+        const int64_t big_tiles = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
+        return {big_tiles >= 512 ? 1 : 2, 1};
+    }
+    auto with_splits = [&](int cfg) { return W16Plan{cfg, split_override > 1 ? split_override : 1}; };
+    // Split K (f32 partial sums, one reduction launch) when even 64 x 128
+    // tiles leave CUs idle and K is long: 128 x 128 tiles two per CU, K split
+    // 2..4 ways to about one unit per CU (MI355X, weights rotated past the
+    // MALL: 1024 x 8960 -> 1536 46.9 us against 54.2 unsplit, 256 x 12288 ->
+    // 4096 41.0 against 76.7, 256 x 4096 -> 4096 24.6 against 28.5). On K =
+    // 1536 the partial sums' traffic costs more than the split saves.
+    const int64_t tiles64 = ((a.rows + 63) / 64) * ((a.columns + 127) / 128);
+    if (a.width >= 4096 && tiles64 < cus) {
+        const int64_t tiles128 = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
+        const int64_t want = cus / tiles128;
+        const int sp = split_override > 1 ? split_override : (int)(want < 2 ? 2 : want > 4 ? 4 : want);
+        if (!ws_limited || fit_splits(a, (int)(a.width / 64), sp) > 1) return {10, sp};
+    }
+    // Cost model over the one-workgroup-per-CU rings, fitted to MI355X
+    // timings (weights rotated past the MALL) of every ring on twelve prefill
+    // shapes, M 512..4096, K 1536..4096, N 1536..17920: tiles run in rounds
+    // of one per CU, a round costs BM * BN * (c * K + e), a partial last
+    // round with fill f costs 0.7 + 0.3 f of a full one. It picks within
+    // 1.2 % of the fastest ring on all twelve (the fixed rules it replaces:
+    // up to 40 % off). Candidates: 256 x 256 with the four waves side by
+    // side along N (each W code converted by one wave), 256 x 192, and
+    // 128 x 256 with eight waves (two per SIMD).
+    struct Cand {
+        double t;
+        int id;
+        int64_t tiles;
+    };
+    auto cost = [&](int id, double c, double e, int64_t bm, int64_t bn) {
+        const int64_t tiles = ((a.rows + bm - 1) / bm) * ((a.columns + bn - 1) / bn);
+        const int64_t full = tiles / cus, rem = tiles % cus;
+        const double rounds = (double)full + (rem ? 0.7 + 0.3 * (double)rem / (double)cus : 0.0);
+        return Cand{(double)(bm * bn) * (c * (double)a.width + e) * rounds, id, tiles};
+    };
+    Cand best = cost(7, 0.3715, 418.5, 256, 256);
+    for (const Cand& c : {cost(9, 0.4273, 399.1, 256, 192), cost(16, 0.4289, 201.6, 128, 256)})
+        if (c.t < best.t) best = c;
+    if (2 * best.tiles >= cus) return with_splits(best.id);
+    // Fewer tiles than half the CUs: 64 x 128 tiles three workgroups per CU
+    // when they fit one round of those slots (config 5's 1024 x 1536 ->
+    // 1536 / 2048 / 512: 13.4 / 13.4 / 11.9 us against 20.9 / 20.8 / 19.9
+    // for 128 x 256), else 128 x 256.
+    if (tiles64 <= 3 * (int64_t)cus) return with_splits(12);
+    return with_splits(16);
+}
+
+int64_t w8a16_partial_elems(int64_t rows, int64_t columns, int64_t width) {
+    if (rows <= 0 || columns <= 0) return 0;
+    W8A16Args a{};
+    a.rows = rows;
+    a.columns = columns;
+    a.width = width;
+    const W16Plan p = plan_w8a16(a, cu_count(), false);
+    return p.cfg >= 4 && p.splits > 1 ? (int64_t)p.splits * rows * columns : 0;
+}
+
 hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream) {
     if (a.rows == 0 || a.columns == 0) return hipSuccess;
-    const bool ring_ok = ring16_fits(a);
-    switch (w8a16_tile_override()) {
+    const W16Plan p = plan_w8a16(a, cu_count(), true);
+    const int sp = p.splits;
+    switch (p.cfg) {
         case 1: return launch_mfma16_cfg<128, 128, 64, 2, 2, 4>(a, stream);
         case 2: return launch_mfma16_cfg<64, 64, 64, 2, 2, 4>(a, stream);
-        case 4: if (ring_ok) return launch_ring16_cfg<256, 128>(a, stream); break;
-        case 5: if (ring_ok) return launch_ring16_cfg<128, 128>(a, stream); break;
-        case 6: if (ring_ok) return launch_ring16_cfg<256, 256>(a, stream); break;
-        case 7: if (ring_ok) return launch_ring16_cfg<256, 256, 8, 1>(a, stream); break;
-        case 8: if (ring_ok) return launch_ring16_cfg<64, 128>(a, stream); break;
-        case 9: if (ring_ok) return launch_ring16_cfg<256, 192>(a, stream); break;
-        case 10: if (ring_ok) return launch_ring16_cfg<128, 128, 8, 2, 3, 2, 2>(a, stream); break;
-        case 11: if (ring_ok) return launch_ring16_cfg<64, 128, 8, 2, 3, 2, 2>(a, stream); break;
-        case 12: if (ring_ok) return launch_ring16_cfg<64, 128, 8, 2, 3, 2, 3>(a, stream); break;
-        default: break;
+        case 4: return launch_ring16_cfg<256, 128>(a, stream, sp);
+        case 5: return launch_ring16_cfg<128, 128>(a, stream, sp);
+        case 6: return launch_ring16_cfg<256, 256>(a, stream, sp);
+        case 7: return launch_ring16_cfg<256, 256, 8, 1>(a, stream, sp);
+        case 8: return launch_ring16_cfg<64, 128>(a, stream, sp);
+        case 9: return launch_ring16_cfg<256, 192>(a, stream, sp);
+        case 10: return launch_ring16_cfg<128, 128, 8, 2, 3, 2, 2>(a, stream, sp);
+        case 11: return launch_ring16_cfg<64, 128, 8, 2, 3, 2, 2>(a, stream, sp);
+        case 16: return launch_ring16_cfg<128, 256, 8, 2, 3, 2, 1, 8>(a, stream, sp);
+        default: return launch_ring16_cfg<64, 128, 8, 2, 3, 2, 3>(a, stream, sp);
     }
-    // Measured on MI355X (config 5 and the BASELINE GEMM shapes): the ring
-    // kernel wins once K is long and its 256 x 128 tiles fill a round of CUs;
-    // the tiled kernels win on the small prefill shapes.
-    int dev = 0, cus = 256;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        cus = 256;
-    // 256 x 256 tiles with the four waves side by side along N (each wave
-    // 256 x 64: every weight code is converted by one wave only) once they
-    // fill a round of CUs: 1030-1140 TFLOP/s at 4096 x 4096 x 12288..14336,
-    // against 970 for 256 x 128 tiles.
-    const int64_t wide_tiles = ((a.rows + 255) / 256) * ((a.columns + 255) / 256);
-    if (ring_ok && a.width >= 3072 && wide_tiles >= cus) return launch_ring16_cfg<256, 256, 8, 1>(a, stream);
-    const int64_t ring_tiles = ((a.rows + 255) / 256) * ((a.columns + 127) / 128);
-    if (ring_ok && a.width >= 3072 && ring_tiles >= cus) return launch_ring16_cfg<256, 128>(a, stream);
-    // Smaller prefill shapes (config 5's M = 1024 linears, K 1536 and 8960),
-    // measured on MI355X against every ring variant:
-    // * 256 x 192 tiles when they fill between half and all of one round of
-    //   CUs on a short K (1024 x 1536 -> 8960: 188 tiles, 43.7 us against
-    //   52.9 for the next best);
-    // * else 64 x 128 tiles three workgroups per CU when they fit in one
-    //   round of those slots (1024 x 8960 -> 1536: 52.4 us against 56.9 at
-    //   one per CU; 1024 x 1536 -> 1536 / 512: 12.7 / 11.8 us against 13.4 /
-    //   12.4);
-    // * else 128 x 128 tiles two per CU (2048 x 4096 -> 4096: 73.6 us
-    //   against 121 for 64 x 128 three per CU).
-    if (ring_ok) {
-        const int64_t tiles192 = ((a.rows + 255) / 256) * ((a.columns + 191) / 192);
-        if (a.width < 3072 && 2 * tiles192 >= cus && tiles192 <= cus) return launch_ring16_cfg<256, 192>(a, stream);
-        const int64_t tiles64 = ((a.rows + 63) / 64) * ((a.columns + 127) / 128);
-        if (tiles64 <= 3 * (int64_t)cus) return launch_ring16_cfg<64, 128, 8, 2, 3, 2, 3>(a, stream);
-        return launch_ring16_cfg<128, 128, 8, 2, 3, 2, 2>(a, stream);
-    }
-    const int64_t big_tiles = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
-    if (big_tiles >= 512) return launch_mfma16_cfg<128, 128, 64, 2, 2, 4>(a, stream);
-    return launch_mfma16_cfg<64, 64, 64, 2, 2, 4>(a, stream);
 }
 
 hipError_t launch_w4a16_gemv(const W8A16Args& a, hipStream_t stream) {

@@ -629,8 +629,16 @@ __global__ __launch_bounds__(128 * WAVES_M, 512 / (128 * WAVES_M)) void w8a8_dma
 // in the first half of tile t-3, so tile t is issued at least 2.5 K tiles
 // before it is read. The K loop is unrolled over 2S tiles (slot and pair
 // parity compile-time) with a uniform exit, so any K % 64 == 0 is taken.
-template <int BN, int S, bool OUT16, bool DUMP, bool PAIR = false>
-__global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
+//
+// SK (split K, `splits` > 1): the work units are (tile, split) pairs, split s
+// covering K tiles [s * kts, min(ktiles, (s + 1) * kts)) with kts =
+// ceil(ktiles / splits) (the host keeps every split non-empty); a unit
+// stores its raw int32 sums to partial[s][rows][columns] and
+// w8a8_split_reduce_kernel adds the splits (int32 wrapping sums are exact in
+// any order) and applies the epilogue, so the output is bit-identical to the
+// unsplit kernel's. Units of one split are consecutive.
+template <int BN, int S, bool OUT16, bool DUMP, bool PAIR = false, bool SK = false>
+__global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a, int splits) {
     constexpr int BM = 256, BK = 64;
     constexpr int WM = 128, WN = BN / 2;
     constexpr int FM = WM / 32, FN = WN / 32;
@@ -669,8 +677,12 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
     const int tiles_m = (int)((a.rows + BM - 1) / BM);
     const int tiles_n = (int)((a.columns + BN - 1) / BN);
     const int total = tiles_m * tiles_n;
+    const int units = SK ? total * splits : total;
     const int K = (int)a.width;
-    const int ktiles = K / BK;
+    const int ktiles_all = K / BK;
+    const int kts = SK ? (ktiles_all + splits - 1) / splits : ktiles_all;
+    // K tiles [kbase, kbase + ktiles) of the unit being copied; its split.
+    int kbase = 0, ktiles = ktiles_all, split = 0;
     const bool has_bias = a.bias != nullptr;
     const bool has_zero = a.w_zero != nullptr;
     constexpr int kGroupM = 4;
@@ -696,12 +708,20 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
     int64_t m0 = 0, n0 = 0;
     float p_rs = 0.0f, p_cs = 0.0f, p_cb = 0.0f;
     int p_rsum = 0, p_cz = 0;
-    auto tile_origin = [&](int l, int64_t& tm0, int64_t& tn0) {
+    auto tile_origin = [&](int u, int64_t& tm0, int64_t& tn0) {
+        const int l = SK ? u % total : u;
         const int group_size = kGroupM * tiles_n;
         const int first_m = (l / group_size) * kGroupM;
         const int gm = min(tiles_m - first_m, kGroupM);
         tm0 = (int64_t)__builtin_amdgcn_readfirstlane(first_m + (l % group_size) % gm) * BM;
         tn0 = (int64_t)__builtin_amdgcn_readfirstlane((l % group_size) / gm) * BN;
+    };
+    auto unit_k = [&](int u) {
+        if constexpr (SK) {
+            split = __builtin_amdgcn_readfirstlane(u / total);
+            kbase = split * kts;
+            ktiles = min(kts, ktiles_all - kbase);
+        }
     };
     // Copy sources of the tile at (m0, n0). Which matrix a copy reads and its
     // first row are wave-uniform (scalar selects, no branches).
@@ -745,7 +765,7 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
         if (tid < BN && p_cz != 0) sZero[p] = 1;
     };
     auto copy_one = [&](int kt, int s, int j) {
-        const int k0 = min(kt, ktiles - 1) * BK;
+        const int k0 = (kbase + min(kt, ktiles - 1)) * BK;
         const bool is_a = (wave * kCpw + j) * 16 < BM;  // wave-uniform
         const uint8_t* base = (is_a ? a.x : a.w) + k0;
         lds_copy16_saddr(voff[j], base, stage_lds[s] + (wave * kCpw + j) * 1024);
@@ -797,10 +817,11 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
     };
 
     int L = xcd_remap(blockIdx.x, gridDim.x);
-    if (L >= total) return;
+    if (L >= units) return;
     if (tid == 0) sWide[0] = sWide[1] = sZero[0] = sZero[1] = 0;
     __syncthreads();
     tile_origin(L, m0, n0);
+    unit_k(L);
     setup_copies();
     load_params(m0, n0);
     store_params(0);
@@ -809,7 +830,7 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
 
     while (true) {
         const int Ln = L + gridDim.x;
-        const bool more = Ln < total;
+        const bool more = Ln < units;
         int64_t nm0 = 0, nn0 = 0;
         if (more) {
             // The next tile's epilogue values, loaded a whole tile early.
@@ -907,6 +928,7 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
         }
 
         const int64_t em0 = m0, en0 = n0;
+        const int esplit = split;
         // Every wave is done reading the ring before the next tile's copies
         // (the clamped copies still in flight land first: one wave's loads
         // complete in issue order, and each wave writes its own LDS chunks).
@@ -915,6 +937,7 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
         if (more) {
             m0 = nm0;
             n0 = nn0;
+            unit_k(Ln);
             setup_copies();
             store_params(parity ^ 1);
             prologue();
@@ -938,6 +961,31 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a) {
         const int64_t tile_base = em0 * a.columns + en0;
         int efr = fr, efh = fh;
         asm volatile("" : "+v"(efr), "+v"(efh));
+        if constexpr (SK) {
+            // Raw sums of this split (plain stores: the reduction reads them
+            // back right after), in-bounds rows and columns only.
+            int32_t* pt = a.partial + (int64_t)esplit * a.rows * a.columns + tile_base;
+            const int rows_last = (int)min((int64_t)BM, a.rows - em0) - 1;
+            const int cols_last = (int)min((int64_t)BN, a.columns - en0) - 1;
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    const int lc = wn * WN + j * 32 + efr;
+                    const int lr0 = wm * WM + i * 32 + 4 * efh;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int lr = lr0 + 8 * (r >> 2) + (r & 3);
+                        if (lc <= cols_last && lr <= rows_last) pt[(unsigned)(lr * N + lc)] = acc[i][j][r];
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            if (!more) break;
+            L = Ln;
+            parity ^= 1;
+            continue;
+        }
         const bool full = em0 + BM <= a.rows && en0 + BN <= a.columns;
         const bool wide = __builtin_amdgcn_readfirstlane(sWide[parity]) != 0;
         const bool zeros = has_zero && __builtin_amdgcn_readfirstlane(sZero[parity]) != 0;
@@ -1157,14 +1205,97 @@ hipError_t launch_ring_cfg(const W8A8Args& a, hipStream_t stream) {
     // Persistent: one workgroup per CU (the kernel's occupancy is one).
     const int64_t grid = tiles < num_cus() ? tiles : num_cus();
     hipLaunchKernelGGL((w8a8_ring_kernel<BN, S, OUT16, DUMP, PAIR>), dim3((unsigned)grid), dim3(256), 0,
-                       stream, a);
+                       stream, a, 1);
     return hipGetLastError();
 }
 
-// The pair-refill ring takes any K % 64 == 0.
+// Split-K reduction: acc = the splits' int32 sums added (wrapping, exact in
+// any order), then the ring's epilogue, four consecutive elements per lane:
+// out = f32(acc - x_sum * w_zero) * x_scale * w_scale (+ bias), as f32 or
+// rounded once to f16; the accumulators to acc_dump when asked.
+template <bool OUT16, bool DUMP>
+__global__ __launch_bounds__(256) void w8a8_split_reduce_kernel(W8A8Args a, int splits) {
+    const int64_t n = a.rows * a.columns;
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= n) return;
+    unsigned v[4] = {0u, 0u, 0u, 0u};
+    int e_end = 4;
+    if (a.columns % 4 == 0) {
+        for (int p = 0; p < splits; ++p) {
+            const int4 t = *reinterpret_cast<const int4*>(a.partial + p * n + i);
+            v[0] += (unsigned)t.x;
+            v[1] += (unsigned)t.y;
+            v[2] += (unsigned)t.z;
+            v[3] += (unsigned)t.w;
+        }
+    } else {
+        e_end = (int)min((int64_t)4, n - i);
+        for (int e = 0; e < e_end; ++e)
+            for (int p = 0; p < splits; ++p) v[e] += (unsigned)a.partial[p * n + i + e];
+    }
+    const bool has_zero = a.w_zero != nullptr;
+    int64_t row = i / a.columns, col = i - row * a.columns;
+    for (int e = 0; e < e_end; ++e) {
+        const int64_t idx = i + e;
+        if (e > 0 && ++col == a.columns) col = 0, ++row;
+        const unsigned prod = has_zero ? (unsigned)a.x_sum[row] * (unsigned)a.w_zero[col] : 0u;
+        const int centered = (int)(v[e] - prod);
+        const float o = w8a8_scale(centered, a.x_scale[row], a.w_scale[col], a.bias ? a.bias[col] : -0.0f);
+        if constexpr (DUMP) a.acc_dump[idx] = (int)v[e];
+        if constexpr (OUT16)
+            stream_store(static_cast<_Float16*>(a.out) + idx, (_Float16)o);
+        else
+            stream_store(static_cast<float*>(a.out) + idx, o);
+    }
+}
+
+// Largest split count <= want that leaves every split of ktiles K tiles
+// non-empty, keeps unit indices in int and whose partial sums fit in
+// a.partial_elems.
+int fit_splits(const W8A8Args& a, int64_t tiles, int ktiles, int want) {
+    int s = want < ktiles ? want : ktiles;
+    while (s > 1) {
+        const int kts = (ktiles + s - 1) / s;
+        if ((s - 1) * kts < ktiles && tiles * s <= INT32_MAX && a.partial &&
+            s * a.rows * a.columns <= a.partial_elems)
+            break;
+        --s;
+    }
+    return s < 1 ? 1 : s;
+}
+
+template <int BN, bool OUT16, bool DUMP>
+hipError_t launch_pair_split(const W8A8Args& a, int splits, hipStream_t stream) {
+    const int64_t tiles = ((a.rows + 255) / 256) * ((a.columns + BN - 1) / BN);
+    const int64_t units = tiles * splits;
+    const int64_t grid = units < num_cus() ? units : num_cus();
+    hipLaunchKernelGGL((w8a8_ring_kernel<BN, 5, OUT16, DUMP, true, true>), dim3((unsigned)grid), dim3(256), 0,
+                       stream, a, splits);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t quads = (a.rows * a.columns + 3) / 4;
+    hipLaunchKernelGGL((w8a8_split_reduce_kernel<OUT16, DUMP>), dim3((unsigned)((quads + 255) / 256)), dim3(256), 0,
+                       stream, a, splits);
+    return hipGetLastError();
+}
+
+// The pair-refill ring takes any K % 64 == 0; splits > 1 splits K when the
+// partial sums fit (else it splits less).
 template <int BN>
-hipError_t launch_pair(const W8A8Args& a, hipStream_t stream) {
+hipError_t launch_pair(const W8A8Args& a, hipStream_t stream, int splits = 1) {
     if (a.width % 64 != 0 || a.width == 0 || !ring_offsets_fit(a)) return launch_bn<BN == 128 ? 128 : 192, 2>(a, stream);
+    if (splits > 1) {
+        const int64_t tiles = ((a.rows + 255) / 256) * ((a.columns + BN - 1) / BN);
+        splits = fit_splits(a, tiles, (int)(a.width / 64), splits);
+    }
+    if (splits > 1) {
+        if (a.acc_dump) {
+            if (a.out_f16) return launch_pair_split<BN, true, true>(a, splits, stream);
+            return launch_pair_split<BN, false, true>(a, splits, stream);
+        }
+        if (a.out_f16) return launch_pair_split<BN, true, false>(a, splits, stream);
+        return launch_pair_split<BN, false, false>(a, splits, stream);
+    }
     if (a.acc_dump) {
         if (a.out_f16) return launch_ring_cfg<BN, 5, true, true, true>(a, stream);
         return launch_ring_cfg<BN, 5, false, true, true>(a, stream);
@@ -1216,6 +1347,30 @@ hipError_t launch_bn(const W8A8Args& a, hipStream_t stream) {
     return launch_out<BN, PF, false, false>(a, stream);
 }
 
+// OMNI_W8A8_SPLITS=<n> forces n-way split K on the pair ring (test aid;
+// read on every launch); 0 or unset = the shape rule below.
+int w8a8_split_override() {
+    const char* v = std::getenv("OMNI_W8A8_SPLITS");
+    return v ? std::atoi(v) : 0;
+}
+
+// Split K when 256 x 128 tiles fill at most half of the CUs and K is long
+// (>= 8192): K split up to 6 ways, at most one unit per CU, on the 256 x 128
+// pair ring. The partial sums cost one int32 write and read per element and
+// split, so shorter K does not pay (MI355X, the reference's shapes: 256 x
+// 4096 x 12288 70 -> 32 us, 256 x 3072 x 12288 69 -> 29 us, 512 x 4096 x
+// 12288 68 -> 49 us; at K = 4096 a split gains at most 6 % and 256 x 12288 x
+// 4096 loses 28 -> 41 us).
+int w8a8_auto_splits(int64_t rows, int64_t columns, int64_t width, int64_t cus) {
+    const int ov = w8a8_split_override();
+    if (ov > 1) return ov;
+    if (width % 64 != 0 || width < 8192) return 1;
+    const int64_t tiles = ((rows + 255) / 256) * ((columns + 127) / 128);
+    if (2 * tiles > cus) return 1;
+    const int64_t want = cus / tiles;
+    return (int)(want > 6 ? 6 : want);
+}
+
 }  // namespace
 
 hipError_t launch_w8a8_scalar(const W8A8Args& a, hipStream_t stream) {
@@ -1225,6 +1380,17 @@ hipError_t launch_w8a8_scalar(const W8A8Args& a, hipStream_t stream) {
     dim3 grid((unsigned)((a.columns + 255) / 256), (unsigned)(row_blocks < 65535 ? row_blocks : 65535));
     hipLaunchKernelGGL(w8a8_scalar_kernel, grid, block, 0, stream, a);
     return hipGetLastError();
+}
+
+int64_t w8a8_partial_elems(int64_t rows, int64_t columns, int64_t width) {
+    if (rows <= 0 || columns <= 0 || width % 64 != 0) return 0;
+    W8A8Args a{};
+    a.rows = rows;
+    a.columns = columns;
+    a.width = width;
+    if (!ring_offsets_fit(a)) return 0;
+    const int sp = w8a8_auto_splits(rows, columns, width, num_cus());
+    return sp > 1 ? (int64_t)sp * rows * columns : 0;
 }
 
 hipError_t launch_w8a8_mfma(const W8A8Args& a, hipStream_t stream) {
@@ -1240,7 +1406,7 @@ hipError_t launch_w8a8_mfma(const W8A8Args& a, hipStream_t stream) {
         case 14: return launch_ring<256, 3>(a, stream);
         case 15: return launch_ring<192, 3>(a, stream);
         case 16: return launch_pair<192>(a, stream);
-        case 17: return launch_pair<128>(a, stream);
+        case 17: return launch_pair<128>(a, stream, w8a8_split_override());
         default: break;
     }
     // Cost model, fitted to MI355X timings of every candidate on ten shapes
@@ -1271,6 +1437,11 @@ hipError_t launch_w8a8_mfma(const W8A8Args& a, hipStream_t stream) {
                                                                                  : launch_bn<192, 2>(a, stream);
     }
     const int64_t kt = a.width / 64;
+    const int sp = w8a8_auto_splits(a.rows, a.columns, a.width, cus);
+    if (sp > 1) {
+        const int64_t tiles = ((a.rows + 255) / 256) * ((a.columns + 127) / 128);
+        if (fit_splits(a, tiles, (int)kt, sp) > 1) return launch_pair<128>(a, stream, sp);
+    }
     Cand best{cost(243.7, 117070.0, 256, 192), 16};
     auto consider = [&](bool ok, double t, int id) {
         if (ok && t < best.t) best = Cand{t, id};

@@ -145,10 +145,13 @@ def w8a8_gemm(codes: torch.Tensor, row_scale: torch.Tensor, row_sum: Optional[to
     odt = {torch.float32: OMNI_F32, torch.float16: OMNI_F16}[out_dtype]
     out = torch.empty((rows, columns), dtype=out_dtype, device=device)
     acc = torch.empty((rows, columns), dtype=torch.int32, device=device) if acc_dump else None
-    st = _lib.check(_lib.lib().omni_w8a8_gemm(
+    L = _lib.lib()
+    ws_bytes = L.omni_w8a8_gemm_workspace_size(rows, columns, width) if lowering != OMNI_LOWERING_SCALAR else 0
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes else None
+    st = _lib.check(L.omni_w8a8_gemm_ws(
         _ptr(codes_c), _ptr(row_scale_c), _ptr(row_sum_c), _ptr(w_c), _ptr(w_scale_c),
         _ptr(w_zero_c), _ptr(bias_c), rows, columns, width, _ptr(out), odt, _ptr(acc),
-        lowering, _stream(device)))
+        lowering, _ptr(workspace), ws_bytes, _stream(device)))
     if st == OMNI_NOT_HANDLED:
         raise ValueError(_lib.last_error())
     return (out, acc) if acc_dump else out
@@ -214,9 +217,12 @@ def w8a16_linear(x: torch.Tensor, w: torch.Tensor, scale: torch.Tensor,
     scale_c = scale.reshape(-1).contiguous()
     bias_c = None if bias is None else bias.reshape(-1).contiguous()
     out = torch.empty((x2.shape[0], columns), dtype=torch.float16, device=device)
-    st = _lib.check(_lib.lib().omni_w8a16_gemm(
+    L = _lib.lib()
+    ws_bytes = L.omni_w8a16_gemm_workspace_size(x2.shape[0], columns, width)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes else None
+    st = _lib.check(L.omni_w8a16_gemm_ws(
         _ptr(x2), _ptr(w), _ptr(scale_c), _ptr(bias_c), x2.shape[0], columns, width, _ptr(out),
-        _stream(device)))
+        _ptr(workspace), ws_bytes, _stream(device)))
     if st == OMNI_NOT_HANDLED:
         raise ValueError(_lib.last_error())
     return out.reshape(*lead, columns)

@@ -159,14 +159,15 @@ def test_skinny_lds_kernel_and_fallback(oracle, monkeypatch, kernel, rows, width
     assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL, (kernel, rows, width, columns)
 
 
-@pytest.mark.parametrize("tile", ["1", "2", "4", "5", "6", "7", "8", "9", "10", "11", "12"])
+@pytest.mark.parametrize("tile", ["1", "2", "4", "5", "6", "7", "8", "9", "10", "11", "12", "16"])
 @pytest.mark.parametrize("rows,width,columns", [(300, 512, 200), (1024, 1536, 1536), (257, 8960, 129),
                                                 (197, 4096, 640), (65, 64, 33), (600, 4096, 700)])
 def test_every_prefill_kernel(oracle, monkeypatch, tile, rows, width, columns):
     # OMNI_W8A16_TILE pins one prefill kernel: the tiled GEMMs (1, 2) and the
     # LDS-DMA ring GEMMs (4 = 256 x 128, 5 = 128 x 128, 6 = 256 x 256, 7 = 256 x 256
     # with the waves side by side, 8 = 64 x 128, 9 = 256 x 192, 10 = 128 x 128
-    # two workgroups per CU, 11 / 12 = 64 x 128 two / three per CU); ragged
+    # two workgroups per CU, 11 / 12 = 64 x 128 two / three per CU, 16 =
+    # 128 x 256 with eight waves); ragged
     # rows/columns, bias, against the f64 ground truth
     monkeypatch.setenv("OMNI_W8A16_TILE", tile)
     rng = np.random.default_rng(rows + width + columns + int(tile))
@@ -186,3 +187,81 @@ def test_config5_small_vlm_layer(oracle):
             got = host(oi.w8a16_linear(dev(x), dev(w), dev(s)))
             ref = gpu_f64_reference(x, w, s, None)
             assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL, (rows, width, columns)
+
+
+@pytest.mark.parametrize("tile", ["4", "5", "8", "9", "10", "11", "12", "16"])
+@pytest.mark.parametrize("splits", ["2", "3", "5", "8"])
+@pytest.mark.parametrize("rows,width,columns,bias", [(1024, 8960, 1536, False), (300, 1536, 202, True),
+                                                     (257, 448, 129, True), (65, 64, 33, False),
+                                                     (130, 4096, 515, True)])
+def test_split_k_every_ring_kernel(oracle, monkeypatch, tile, splits, rows, width, columns, bias):
+    # OMNI_W8A16_SPLITS forces split K on a pinned ring kernel: units of
+    # (tile, K range), f32 partial sums, an in-order reduction applying scale
+    # and bias. K tile counts 140, 24, 7 (uneven splits, fewer than asked
+    # when a split would be empty) and 1 (no split), ragged rows and
+    # columns, columns % 4 != 0 (the reduction's scalar path).
+    monkeypatch.setenv("OMNI_W8A16_TILE", tile)
+    monkeypatch.setenv("OMNI_W8A16_SPLITS", splits)
+    rng = np.random.default_rng(rows + width + columns + 10 * int(tile) + int(splits))
+    x, w, s, b = make(rng, rows, width, columns, bias=bias)
+    xd, wd, sd, bd = dev(x), dev(w), dev(s), None if b is None else dev(b)
+    got = oi.w8a16_linear(xd, wd, sd, bd)
+    again = oi.w8a16_linear(xd, wd, sd, bd)
+    ref = gpu_f64_reference(x, w, s, b)
+    assert tolerance.rel_err(host(got), ref) <= tolerance.FP16_REL_TOL, (tile, splits, rows, width, columns)
+    assert torch.equal(got, again), "split K must be deterministic"
+
+
+def test_split_k_workspace_contract(monkeypatch):
+    # omni_w8a16_gemm_workspace_size reports splits * rows * columns floats
+    # for a split shape and 0 otherwise; omni_w8a16_gemm_ws splits less with
+    # a smaller workspace, not at all with none, and every result is within
+    # the bar.
+    from omni_int8 import _lib
+    L = _lib.lib()
+    monkeypatch.setenv("OMNI_W8A16_TILE", "12")
+    monkeypatch.setenv("OMNI_W8A16_SPLITS", "4")
+    rows, width, columns = 192, 2048, 256
+    assert L.omni_w8a16_gemm_workspace_size(rows, columns, width) == 4 * rows * columns * 4
+    assert L.omni_w8a16_gemm_workspace_size(64, columns, width) == 0  # skinny route
+    assert L.omni_w8a16_gemm_workspace_size(4, columns, width) == 0  # GEMV
+    monkeypatch.delenv("OMNI_W8A16_TILE")
+    monkeypatch.delenv("OMNI_W8A16_SPLITS")
+    # the launcher's own choice: config 5's down projection splits, its
+    # K = 1536 linears do not
+    assert L.omni_w8a16_gemm_workspace_size(1024, 1536, 8960) % (1024 * 1536 * 4) == 0
+    assert L.omni_w8a16_gemm_workspace_size(1024, 1536, 8960) >= 2 * 1024 * 1536 * 4
+    assert L.omni_w8a16_gemm_workspace_size(1024, 8960, 1536) == 0
+    rng = np.random.default_rng(78)
+    x, w, s, b = make(rng, 1024, 8960, 1536)
+    xd, wd, sd = dev(x), dev(w), dev(s)
+    ref = gpu_f64_reference(x, w, s, None)
+    out = torch.empty((1024, 1536), dtype=torch.float16, device="cuda")
+    st = L.omni_w8a16_gemm(xd.data_ptr(), wd.data_ptr(), sd.data_ptr(), None, 1024, 1536, 8960, out.data_ptr(),
+                           torch.cuda.current_stream().cuda_stream)
+    assert st == 0, _lib.last_error()
+    assert tolerance.rel_err(host(out), ref) <= tolerance.FP16_REL_TOL  # no workspace: unsplit
+    assert tolerance.rel_err(host(oi.w8a16_linear(xd, wd, sd)), ref) <= tolerance.FP16_REL_TOL  # split
+    monkeypatch.setenv("OMNI_W8A16_TILE", "12")
+    monkeypatch.setenv("OMNI_W8A16_SPLITS", "4")
+    rng = np.random.default_rng(77)
+    x, w, s, b = make(rng, rows, width, columns, bias=True)
+    xd, wd, sd, bd = dev(x), dev(w), dev(s), dev(b)
+    ref = gpu_f64_reference(x, w, s, b)
+    stream = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for floats in (4 * rows * columns, 2 * rows * columns + 5, 0):
+        ws = torch.empty(max(floats, 1) * 4, dtype=torch.uint8, device="cuda")
+        out = torch.empty((rows, columns), dtype=torch.float16, device="cuda")
+        st = L.omni_w8a16_gemm_ws(xd.data_ptr(), wd.data_ptr(), sd.data_ptr(), bd.data_ptr(), rows, columns,
+                                  width, out.data_ptr(), ws.data_ptr() if floats else None, floats * 4, stream)
+        assert st == 0, _lib.last_error()
+        assert tolerance.rel_err(host(out), ref) <= tolerance.FP16_REL_TOL, floats
+        outs.append(out)
+    monkeypatch.setenv("OMNI_W8A16_SPLITS", "1")
+    plain = oi.w8a16_linear(xd, wd, sd, bd)
+    assert torch.equal(outs[2], plain), "no workspace runs unsplit"
+    bad = torch.empty(1024, dtype=torch.uint8, device="cuda")
+    st = L.omni_w8a16_gemm_ws(xd.data_ptr(), wd.data_ptr(), sd.data_ptr(), bd.data_ptr(), rows, columns, width,
+                              outs[0].data_ptr(), bad.data_ptr() + 4, 512, stream)
+    assert st == _lib.OMNI_BAD_ARGUMENT

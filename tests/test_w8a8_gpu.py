@@ -496,3 +496,81 @@ def test_w8a8_rejects_bad_vectors():
         oi.w8a8_gemm(codes, rs, torch.zeros(3, dtype=torch.int32, device="cuda"), w, s, z)
     with pytest.raises(ValueError):  # zero points without row sums
         oi.w8a8_gemm(codes, rs, None, w, s, z)
+
+
+@pytest.mark.parametrize("splits", [2, 3, 4, 8])
+def test_w8a8_split_k_bit_identical(oracle, splits, monkeypatch):
+    # OMNI_W8A8_SPLITS forces split K on the 256 x 128 pair ring: int32
+    # partial sums of (tile, K range) units, then a reduction applying the
+    # epilogue. Every output (f32 and f16, bias, zero points or none, wide
+    # row sums and zero points) and the accumulators must equal the unsplit
+    # kernel's bit for bit; K tile counts 64, 24, 7 (uneven splits, fewer
+    # than asked when a split would be empty) and 1 (no split), ragged rows
+    # and columns, columns % 4 != 0 (the reduction's scalar path).
+    monkeypatch.setenv("OMNI_W8A8_TILE", "17")
+    for rows, width, columns in [(256, 4096, 4096), (300, 1536, 202), (513, 448, 129), (70, 64, 33),
+                                 (257, 4096, 515)]:
+        rng = np.random.default_rng(splits * 1000 + width + columns)
+        codes = dev(rng.integers(-128, 128, (rows, width), dtype=np.int8))
+        w = dev(rng.integers(-128, 128, (columns, width), dtype=np.int8))
+        rs = dev(rng.uniform(1e-4, 1e-2, rows).astype(np.float32))
+        scale = dev(rng.uniform(0.002, 0.02, columns).astype(np.float32))
+        bias = dev(rng.standard_normal(columns).astype(np.float32))
+        small = (dev(rng.integers(-5000, 5000, rows).astype(np.int32)),
+                 dev(rng.integers(-3, 4, columns).astype(np.int32)))
+        wide = (dev(rng.integers(-2**31, 2**31, rows).astype(np.int32)),
+                dev(rng.integers(-2**31, 2**31, columns).astype(np.int32)))
+        for total, zero in (small, wide, (None, None)):
+            for b in (None, bias):
+                for odt in (torch.float32, torch.float16):
+                    monkeypatch.delenv("OMNI_W8A8_SPLITS", raising=False)
+                    ref, ref_acc = oi.w8a8_gemm(codes, rs, total, w, scale, zero, bias=b, out_dtype=odt,
+                                                acc_dump=True, lowering=oi.OMNI_LOWERING_MFMA)
+                    monkeypatch.setenv("OMNI_W8A8_SPLITS", str(splits))
+                    got, acc = oi.w8a8_gemm(codes, rs, total, w, scale, zero, bias=b, out_dtype=odt,
+                                            acc_dump=True, lowering=oi.OMNI_LOWERING_MFMA)
+                    plain = oi.w8a8_gemm(codes, rs, total, w, scale, zero, bias=b, out_dtype=odt,
+                                         lowering=oi.OMNI_LOWERING_MFMA)
+                    case = (splits, rows, width, columns, total is None, b is None, odt)
+                    assert torch.equal(acc, ref_acc), case
+                    assert torch.equal(got.view(torch.int8), ref.view(torch.int8)), case
+                    assert torch.equal(plain.view(torch.int8), ref.view(torch.int8)), case
+        exact = codes.double() @ w.double().T
+        assert torch.equal(ref_acc.double(), exact)
+
+
+def test_w8a8_split_k_workspace_contract(monkeypatch):
+    # omni_w8a8_gemm_workspace_size: the reference's 256-row benchmark shape
+    # with K = 12288 splits, its K = 4096 ones and the north-star shapes do
+    # not; omni_w8a8_gemm_ws splits less with a smaller workspace and not at
+    # all with none, bit-identically.
+    from omni_int8 import _lib
+    L = _lib.lib()
+    size = L.omni_w8a8_gemm_workspace_size(256, 4096, 12288)
+    assert size >= 2 * 256 * 4096 * 4 and size % (256 * 4096 * 4) == 0, size
+    for m, n, k in ((256, 4096, 4096), (256, 12288, 4096), (4096, 12288, 3072), (4096, 3072, 12288)):
+        assert L.omni_w8a8_gemm_workspace_size(m, n, k) == 0, (m, n, k)
+    rows, width, columns = 256, 8192, 1024
+    rng = np.random.default_rng(91)
+    codes = dev(rng.integers(-128, 128, (rows, width), dtype=np.int8))
+    w = dev(rng.integers(-128, 128, (columns, width), dtype=np.int8))
+    rs = dev(rng.uniform(1e-4, 1e-2, rows).astype(np.float32))
+    scale = dev(rng.uniform(0.002, 0.02, columns).astype(np.float32))
+    total = dev(rng.integers(-5000, 5000, rows).astype(np.int32))
+    zero = dev(rng.integers(-3, 4, columns).astype(np.int32))
+    ref = oi.w8a8_gemm(codes, rs, total, w, scale, zero)
+    stream = torch.cuda.current_stream().cuda_stream
+    for ints in (4 * rows * columns, 2 * rows * columns + 3, 0):
+        ws = torch.empty(max(ints, 1) * 4, dtype=torch.uint8, device="cuda")
+        out = torch.empty((rows, columns), dtype=torch.float32, device="cuda")
+        st = L.omni_w8a8_gemm_ws(codes.data_ptr(), rs.data_ptr(), total.data_ptr(), w.data_ptr(),
+                                 scale.data_ptr(), zero.data_ptr(), None, rows, columns, width, out.data_ptr(),
+                                 oi.OMNI_F32, None, oi.OMNI_LOWERING_AUTO, ws.data_ptr() if ints else None,
+                                 ints * 4, stream)
+        assert st == 0, _lib.last_error()
+        assert torch.equal(out.view(torch.int32), ref.view(torch.int32)), ints
+    bad = torch.empty(1024, dtype=torch.uint8, device="cuda")
+    st = L.omni_w8a8_gemm_ws(codes.data_ptr(), rs.data_ptr(), total.data_ptr(), w.data_ptr(), scale.data_ptr(),
+                             zero.data_ptr(), None, rows, columns, width, out.data_ptr(), oi.OMNI_F32, None,
+                             oi.OMNI_LOWERING_AUTO, bad.data_ptr() + 4, 512, stream)
+    assert st == _lib.OMNI_BAD_ARGUMENT
