@@ -1697,7 +1697,9 @@ hipError_t launch_f16_skinny(const W8A16Args& a, hipStream_t stream) { return la
 
 // OMNI_F16_TILE=<n> pins the fp16 GEMM kernel (tuning and test aid):
 // 1 = tiled 128 x 128, 2 = tiled 64 x 64, 4/5/6 = ring 256 x 128 / 128 x 128 /
-// 128 x 256 (K % 64 == 0 only). Read on every call.
+// 128 x 256, 7/8 = ring 256 x 256 / 256 x 128 on 32-element K tiles, 10 =
+// eight-wave ring 256 x 128, 12 = eight-wave ring 256 x 256 on 32-element K
+// tiles (rings: K % 64 == 0 only). Read on every call.
 hipError_t launch_f16_mfma(const W8A16Args& a, hipStream_t stream) {
     if (a.rows == 0 || a.columns == 0) return hipSuccess;
     const bool ring_ok = ring16_fits(a);
@@ -1710,20 +1712,29 @@ hipError_t launch_f16_mfma(const W8A16Args& a, hipStream_t stream) {
         case 6: if (ring_ok) return launch_ring16_cfg<128, 256, 16>(a, stream); break;
         case 7: if (ring_ok) return launch_ring16_cfg<256, 256, 16, 2, 3, 1>(a, stream); break;
         case 8: if (ring_ok) return launch_ring16_cfg<256, 128, 16, 2, 3, 1>(a, stream); break;
+        case 10: if (ring_ok) return launch_ring16_cfg<256, 128, 16, 4, 3, 2, 1, 8>(a, stream); break;
+        case 12: if (ring_ok) return launch_ring16_cfg<256, 256, 16, 4, 3, 1, 1, 8>(a, stream); break;
         default: break;
     }
-    int dev = 0, cus = 256;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        cus = 256;
-    // 256 x 256 tiles on 32-element K tiles once they fill a round of CUs
-    // (4096 x 4096 x 12288: 373 us against 442 for 256 x 128; half the LDS
-    // reads per flop), else 256 x 128 on 64-element K tiles.
-    const int64_t wide_tiles = ((a.rows + 255) / 256) * ((a.columns + 255) / 256);
-    if (ring_ok && a.width >= 3072 && wide_tiles >= cus)
-        return launch_ring16_cfg<256, 256, 16, 2, 3, 1>(a, stream);
-    const int64_t ring_tiles = ((a.rows + 255) / 256) * ((a.columns + 127) / 128);
-    if (ring_ok && a.width >= 3072 && ring_tiles >= cus) return launch_ring16_cfg<256, 128, 16>(a, stream);
+    const int64_t cus = cu_count();
+    // Eight-wave rings (two waves per SIMD): 256 x 256 tiles on 32-element K
+    // tiles (each wave 64 x 128) or 256 x 128 tiles on 64-element K tiles
+    // (each wave 64 x 64), whichever a rounds cost model picks: tiles run in
+    // rounds of one per CU, a partial last round with fill f costs 0.7 +
+    // 0.3 f of a full one, and a 256 x 256 tile costs 1.93 times a 256 x 128
+    // one (MI355X, 4096 x 4096 x 12288: 359.6 / 373.4 us, against 401 for
+    // the four-wave 256 x 256 ring and 319 for torch.matmul; 2048 x 4096 x
+    // 4096: 65.6 us for 256 x 128 against 67.3 for torch.matmul; 4352 x
+    // 4096 x 12288: 426.8 against 422.9).
+    if (ring_ok && a.width >= 3072) {
+        auto rounds = [&](int64_t bn) {
+            const int64_t tiles = ((a.rows + 255) / 256) * ((a.columns + bn - 1) / bn);
+            const int64_t full = tiles / cus, rem = tiles % cus;
+            return (double)full + (rem ? 0.7 + 0.3 * (double)rem / (double)cus : 0.0);
+        };
+        if (1.93 * rounds(256) <= rounds(128)) return launch_ring16_cfg<256, 256, 16, 4, 3, 1, 1, 8>(a, stream);
+        return launch_ring16_cfg<256, 128, 16, 4, 3, 2, 1, 8>(a, stream);
+    }
     const int64_t big_tiles = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
     if (big_tiles >= 512) return launch_mfma16_cfg<128, 128, 64, 2, 2, 4, 16>(a, stream);
     return launch_mfma16_cfg<64, 64, 64, 2, 2, 4, 16>(a, stream);
