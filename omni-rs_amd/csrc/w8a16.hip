@@ -1520,11 +1520,10 @@ hipError_t launch_w8a16_skinny(const W8A16Args& a, hipStream_t stream) { return 
 // 1 = tiled 128 x 128, 2 = tiled 64 x 64, 4/5/6 = ring 256 x 128 / 128 x 128 /
 // 256 x 256 (2 x 2 waves), 7 = ring 256 x 256 (1 x 4 waves), 8 = ring
 // 64 x 128, 9 = ring 256 x 192, 10 = ring 128 x 128 two workgroups per CU,
-// 11 / 12 = ring 64 x 128 two / three per CU, 16 = ring 128 x 256 with eight
-// waves (rings: K % 64 == 0 only). OMNI_W8A16_SPLITS=<n> adds n-way split K
-// to a pinned ring (or to the shape rule's choice) when the call brings a
-// workspace.
-// Read on every call.
+// 11 / 12 = ring 64 x 128 two / three per CU, 16 / 17 = ring 128 x 256 /
+// 256 x 256 with eight waves (rings: K % 64 == 0 only). OMNI_W8A16_SPLITS=<n>
+// adds n-way split K to a pinned ring (or to the shape rule's choice) when
+// the call brings a workspace. Both are read on every call.
 int w8a16_tile_override() {
     const char* v = std::getenv("OMNI_W8A16_TILE");
     return v ? std::atoi(v) : 0;
@@ -1545,7 +1544,7 @@ W16Plan plan_w8a16(const W8A16Args& a, int cus, bool ws_limited) {
     const int split_override = sv ? std::atoi(sv) : 0;
     const bool ring_ok = ring16_fits(a);
     const int ov = w8a16_tile_override();
-    if (ov == 1 || ov == 2 || (ov >= 4 && ov <= 12 && ring_ok) || (ov == 16 && ring_ok))
+    if (ov == 1 || ov == 2 || (ov >= 4 && ov <= 12 && ring_ok) || ((ov == 16 || ov == 17) && ring_ok))
         return {ov, ov >= 4 && split_override > 1 ? split_override : 1};
     if (!ring_ok) {
         const int64_t big_tiles = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
@@ -1571,9 +1570,10 @@ W16Plan plan_w8a16(const W8A16Args& a, int cus, bool ws_limited) {
     // of one per CU, a round costs BM * BN * (c * K + e), a partial last
     // round with fill f costs 0.7 + 0.3 f of a full one. It picks within
     // 1.2 % of the fastest ring on all twelve (the fixed rules it replaces:
-    // up to 40 % off). Candidates: 256 x 256 with the four waves side by
-    // side along N (each W code converted by one wave), 256 x 192, and
-    // 128 x 256 with eight waves (two per SIMD).
+    // up to 40 % off). Candidates: 256 x 192 (four waves), 128 x 256 and
+    // 256 x 256 with eight waves (two per SIMD; the 256 x 256 one measured
+    // 4-15 % faster than the four-wave 256 x 256 ring with the waves side by
+    // side along N on seven shapes, so it takes that ring's fit less 4 %).
     struct Cand {
         double t;
         int id;
@@ -1585,7 +1585,7 @@ W16Plan plan_w8a16(const W8A16Args& a, int cus, bool ws_limited) {
         const double rounds = (double)full + (rem ? 0.7 + 0.3 * (double)rem / (double)cus : 0.0);
         return Cand{(double)(bm * bn) * (c * (double)a.width + e) * rounds, id, tiles};
     };
-    Cand best = cost(7, 0.3715, 418.5, 256, 256);
+    Cand best = cost(17, 0.3566, 401.8, 256, 256);
     for (const Cand& c : {cost(9, 0.4273, 399.1, 256, 192), cost(16, 0.4289, 201.6, 128, 256)})
         if (c.t < best.t) best = c;
     if (2 * best.tiles >= cus) return with_splits(best.id);
@@ -1623,6 +1623,7 @@ hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream) {
         case 10: return launch_ring16_cfg<128, 128, 8, 2, 3, 2, 2>(a, stream, sp);
         case 11: return launch_ring16_cfg<64, 128, 8, 2, 3, 2, 2>(a, stream, sp);
         case 16: return launch_ring16_cfg<128, 256, 8, 2, 3, 2, 1, 8>(a, stream, sp);
+        case 17: return launch_ring16_cfg<256, 256, 8, 4, 3, 2, 1, 8>(a, stream, sp);
         default: return launch_ring16_cfg<64, 128, 8, 2, 3, 2, 3>(a, stream, sp);
     }
 }
