@@ -637,15 +637,22 @@ __global__ __launch_bounds__(128 * WAVES_M, 512 / (128 * WAVES_M)) void w8a8_dma
 // w8a8_split_reduce_kernel adds the splits (int32 wrapping sums are exact in
 // any order) and applies the epilogue, so the output is bit-identical to the
 // unsplit kernel's. Units of one split are consecutive.
-template <int BN, int S, bool OUT16, bool DUMP, bool PAIR = false, bool SK = false>
-__global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a, int splits) {
+//
+// NW = 8: eight waves (two per SIMD) share the ring, 4 x 2 of them over the
+// tile, each owning half as many accumulators, so one wave's MFMAs can issue
+// while the other waits on LDS or the barrier.
+template <int BN, int S, bool OUT16, bool DUMP, bool PAIR = false, bool SK = false, int NW = 4>
+__global__ __launch_bounds__(64 * NW, 1) void w8a8_ring_kernel(W8A8Args a, int splits) {
     constexpr int BM = 256, BK = 64;
-    constexpr int WM = 128, WN = BN / 2;
+    constexpr int WMW = NW / 2, WNW = 2;      // waves along M and N
+    constexpr int WM = BM / WMW, WN = BN / WNW;
     constexpr int FM = WM / 32, FN = WN / 32;
     constexpr int kRows = BM + BN;            // tile rows per stage (A then W)
     constexpr int kStage = kRows * BK;
-    constexpr int kCpw = kRows / 16 / 4;      // 1 KiB copies per wave per K tile
-    static_assert(kRows % 64 == 0 && WN % 32 == 0, "tile shape");
+    constexpr int kCpw = kRows / 16 / NW;     // 1 KiB copies per wave per K tile
+    static_assert(NW == 4 || NW == 8, "four or eight waves");
+    static_assert(kRows % (16 * NW) == 0 && WN % 32 == 0 && WM % 32 == 0, "tile shape");
+    static_assert(FM + FN <= FM * FN && kCpw <= FM * FN, "one read and one copy per MFMA slot");
     static_assert(S >= 3 && S <= 5, "3 to 5 stages");
     static_assert(!PAIR || S == 5, "the pair schedule is laid out for 5 slots");
     // Pair schedule: copy units (copy j of both tiles of a pair) issued after
@@ -673,7 +680,7 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a, int split
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: an SGPR
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WNW, wn = wave % WNW;
     const int tiles_m = (int)((a.rows + BM - 1) / BM);
     const int tiles_n = (int)((a.columns + BN - 1) / BN);
     const int total = tiles_m * tiles_n;
@@ -702,6 +709,8 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a, int split
     // columns * K below 2^32).
     const int cp_row = lane >> 2;
     const int cp_chunk = (lane & 3) ^ ((lane >> 4) & 3);
+    // Stage row block (16 rows) of this wave's copy j (wave-uniform).
+    auto copy_block = [&](int j) { return wave * kCpw + j; };
     unsigned voff[kCpw];
     const unsigned stage_lds[5] = {lds_addr(st0), lds_addr(st1), lds_addr(st2), S > 3 ? lds_addr(st3) : 0u,
                                    S > 4 ? lds_addr(st4) : 0u};
@@ -728,7 +737,7 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a, int split
     auto setup_copies = [&]() {
 #pragma unroll
         for (int j = 0; j < kCpw; ++j) {
-            const int c16 = (wave * kCpw + j) * 16;  // first stage row of copy j
+            const int c16 = copy_block(j) * 16;  // first stage row of copy j
             const bool is_a = c16 < BM;
             const int64_t first = is_a ? m0 + c16 : n0 + (c16 - BM);
             const int64_t last = is_a ? a.rows - 1 : a.columns - 1;
@@ -742,9 +751,11 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a, int split
     // epilogue makes (it is never a signalling NaN), so the add is
     // unconditional and the result is bit-identical to skipping it.
     auto load_params = [&](int64_t pm0, int64_t pn0) {
-        const int64_t row = min(pm0 + tid, a.rows - 1);
-        p_rs = a.x_scale[row];
-        p_rsum = has_zero ? a.x_sum[row] : 0;
+        if (tid < BM) {
+            const int64_t row = min(pm0 + tid, a.rows - 1);
+            p_rs = a.x_scale[row];
+            p_rsum = has_zero ? a.x_sum[row] : 0;
+        }
         if (tid < BN) {
             const int64_t col = min(pn0 + tid, a.columns - 1);
             p_cs = a.w_scale[col];
@@ -754,8 +765,10 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a, int split
     };
     auto fits24 = [](int v) { return (unsigned)v + (1u << 23) < (1u << 24); };
     auto store_params = [&](int p) {
-        sRowScale[p][tid] = p_rs;
-        sRowSum[p][tid] = p_rsum;
+        if (tid < BM) {
+            sRowScale[p][tid] = p_rs;
+            sRowSum[p][tid] = p_rsum;
+        }
         if (tid < BN) {
             sColScale[p][tid] = p_cs;
             sColZero[p][tid] = p_cz;
@@ -766,9 +779,9 @@ __global__ __launch_bounds__(256, 1) void w8a8_ring_kernel(W8A8Args a, int split
     };
     auto copy_one = [&](int kt, int s, int j) {
         const int k0 = (kbase + min(kt, ktiles - 1)) * BK;
-        const bool is_a = (wave * kCpw + j) * 16 < BM;  // wave-uniform
+        const bool is_a = copy_block(j) * 16 < BM;  // wave-uniform
         const uint8_t* base = (is_a ? a.x : a.w) + k0;
-        lds_copy16_saddr(voff[j], base, stage_lds[s] + (wave * kCpw + j) * 1024);
+        lds_copy16_saddr(voff[j], base, stage_lds[s] + copy_block(j) * 1024);
     };
     auto copy_tile = [&](int kt, int s) {
 #pragma unroll
@@ -1199,13 +1212,13 @@ bool ring_offsets_fit(const W8A8Args& a) {
     return a.rows * a.width < lim && a.columns * a.width < lim;
 }
 
-template <int BN, int S, bool OUT16, bool DUMP, bool PAIR = false>
+template <int BN, int S, bool OUT16, bool DUMP, bool PAIR = false, int NW = 4>
 hipError_t launch_ring_cfg(const W8A8Args& a, hipStream_t stream) {
     const int64_t tiles = ((a.rows + 255) / 256) * ((a.columns + BN - 1) / BN);
     // Persistent: one workgroup per CU (the kernel's occupancy is one).
     const int64_t grid = tiles < num_cus() ? tiles : num_cus();
-    hipLaunchKernelGGL((w8a8_ring_kernel<BN, S, OUT16, DUMP, PAIR>), dim3((unsigned)grid), dim3(256), 0,
-                       stream, a, 1);
+    hipLaunchKernelGGL((w8a8_ring_kernel<BN, S, OUT16, DUMP, PAIR, false, NW>), dim3((unsigned)grid),
+                       dim3(64 * NW), 0, stream, a, 1);
     return hipGetLastError();
 }
 
@@ -1320,6 +1333,17 @@ hipError_t launch_ring(const W8A8Args& a, hipStream_t stream) {
     return launch_ring_cfg<BN, S, false, false>(a, stream);
 }
 
+// The eight-wave 256 x 256 ring (4 slots, single refill): K tiles % 4 == 0.
+hipError_t launch_ring8_256(const W8A8Args& a, hipStream_t stream) {
+    if (!ring_fits(a, 4)) return launch_bn<192, 2>(a, stream);
+    if (a.acc_dump) {
+        if (a.out_f16) return launch_ring_cfg<256, 4, true, true, false, 8>(a, stream);
+        return launch_ring_cfg<256, 4, false, true, false, 8>(a, stream);
+    }
+    if (a.out_f16) return launch_ring_cfg<256, 4, true, false, false, 8>(a, stream);
+    return launch_ring_cfg<256, 4, false, false, false, 8>(a, stream);
+}
+
 template <int BN, int S, int WAVES_M = 2>
 hipError_t launch_dma(const W8A8Args& a, hipStream_t stream) {
     if (!dma_fits(a, S)) return launch_bn<BN == 128 ? 128 : 192, 2>(a, stream);
@@ -1407,6 +1431,7 @@ hipError_t launch_w8a8_mfma(const W8A8Args& a, hipStream_t stream) {
         case 15: return launch_ring<192, 3>(a, stream);
         case 16: return launch_pair<192>(a, stream);
         case 17: return launch_pair<128>(a, stream, w8a8_split_override());
+        case 19: return launch_ring8_256(a, stream);
         default: break;
     }
     // Cost model, fitted to MI355X timings of every candidate on ten shapes
@@ -1448,10 +1473,15 @@ hipError_t launch_w8a8_mfma(const W8A8Args& a, hipStream_t stream) {
     };
     consider(true, cost(281.8, 123726.0, 256, 128), 17);
     const bool s4 = kt >= 4 && kt % 4 == 0, s3 = kt >= 3 && kt % 3 == 0;
-    consider(s4, cost(256.1, 173634.0, 256, 256), 11);
+    // The eight-wave 256 x 256 ring replaces the four-wave one (11), at 0.94
+    // of its fit: measured 0.80-0.92 of its time on seven shapes (config 4's
+    // MLP down 4352 x 12288 -> 3072: 160 against 179 us; config 3's 2048 x
+    // 4096 -> 14336: 126 against 139), a factor that keeps both north-star
+    // shapes on the 256 x 192 pair ring, which stays faster there.
+    consider(s4, cost(240.7, 163216.0, 256, 256), 19);
     consider(!s4 && s3, cost(250.7, 210425.0, 256, 256), 14);
     switch (best.id) {
-        case 11: return launch_ring<256, 4>(a, stream);
+        case 19: return launch_ring8_256(a, stream);
         case 14: return launch_ring<256, 3>(a, stream);
         case 17: return launch_pair<128>(a, stream);
         default: return launch_pair<192>(a, stream);

@@ -209,7 +209,7 @@ def test_w8a8_extreme_codes_no_overflow(oracle):
 # shapes with ragged M/N edges, K tails and multi-round tile grids.
 VARIANT_SHAPES = [(300, 1024, 700), (1000, 4096, 1500), (513, 4160, 389), (700, 3072, 650),
                   (2048, 2048, 3072), (4400, 512, 4100)]
-TILE_VARIANTS = [3, 4, 9, 10, 11, 12, 13, 14, 15, 16, 17]  # OMNI_W8A8_TILE values
+TILE_VARIANTS = [3, 4, 9, 10, 11, 12, 13, 14, 15, 16, 17, 19]  # OMNI_W8A8_TILE values
 
 
 @pytest.mark.parametrize("tile", [0] + TILE_VARIANTS)
