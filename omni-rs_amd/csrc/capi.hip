@@ -418,8 +418,12 @@ int omni_convrot_linear(const void* x, int x_dtype, int64_t rows, int64_t width,
 }
 
 size_t omni_w8a16_gemm_workspace_size(int64_t rows, int64_t columns, int64_t width) {
-    if (rows <= 0 || columns <= 0 || width <= 0 || width % 16 != 0 || w8a16_kind(rows, width) != 2) return 0;
-    return (size_t)omni::w8a16_partial_elems(rows, columns, width) * sizeof(float);
+    if (rows <= 0 || columns <= 0 || width <= 0 || width % 16 != 0) return 0;
+    switch (w8a16_kind(rows, width)) {
+        case 1: return (size_t)omni::w8a16_skinny_partial_elems(rows, columns, width) * sizeof(float);
+        case 2: return (size_t)omni::w8a16_partial_elems(rows, columns, width) * sizeof(float);
+        default: return 0;
+    }
 }
 
 int omni_w8a16_gemm(const uint16_t* x, const int8_t* w, const uint16_t* scale,

@@ -57,6 +57,8 @@ hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream);
 // Floats of split-K partial sums launch_w8a16_mfma uses for this shape on the
 // current device (0: no split); with fewer in W8A16Args it splits less.
 int64_t w8a16_partial_elems(int64_t rows, int64_t columns, int64_t width);
+// The same for launch_w8a16_skinny (up to 16 rows: split-K skinny kernel).
+int64_t w8a16_skinny_partial_elems(int64_t rows, int64_t columns, int64_t width);
 
 // W4A16 (w8a16.hip): packed int4 weights (two per byte, low nibble first,
 // offset by 8) with bf16 scales per group of K values.

@@ -604,6 +604,127 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_lds_kernel(W8A16Args a) {
     }
 }
 
+// Split-K skinny GEMM for up to 16 activation rows (int8 weights): a unit
+// is 64 columns x KS = K / splits of K (KS % 256 == 0, KS <= 1024), so each
+// CU takes in 16 x KS x 2 bytes of x and 64 x KS bytes of weights (at
+// 16 x 4096 x 4096 and four splits: 32 KB + 64 KB, against 128 KB + 64 KB
+// for a 16-column unit over all of K). The x slice is staged into LDS as in
+// w8a16_skinny_lds_kernel; wave w takes column block w % 4 (16 columns) and
+// K quarter w / 4 in 64-element steps, two v_mfma_f32_16x16x32_f16 per step;
+// the four quarters are added through LDS and the unit's f32 sums go to
+// partial[split][row][column], which w8a16_split_reduce_kernel adds in
+// order before scale and bias.
+constexpr int kSkinnySplitMaxKS = 1024;
+
+__global__ __launch_bounds__(1024) void w8a16_skinny_split_kernel(W8A16Args a, int splits) {
+    constexpr int RS = kSkinnySplitMaxKS * 2 + 16;  // LDS bytes per x row
+    constexpr int kMaxPieces = 16 * kSkinnySplitMaxKS / 8 / 1024;
+    constexpr int kMaxSteps = kSkinnySplitMaxKS / 4 / 64;
+    __shared__ __attribute__((aligned(16))) uint8_t sx[16 * RS];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int64_t K = a.width;
+    const int KS = (int)(K / splits);
+    const int tiles_n = (int)((a.columns + 63) / 64);
+    const int sp = (int)(blockIdx.x / tiles_n);
+    const int64_t n0 = (int64_t)(blockIdx.x % tiles_n) * 64;
+    const int64_t k0 = (int64_t)sp * KS;
+    const int cb = wave & 3, kq = wave >> 2;
+    const int steps = KS / 256;  // 64-element steps per wave
+    const int r16 = lane & 15, g = lane >> 4;
+    const int pieces_per_row = KS / 8;
+    // Piece idx of x[0:16][k0 : k0 + KS] is 8 consecutive values; row =
+    // idx / pieces_per_row exactly via f32 (idx < 2^11, pieces_per_row >= 32).
+    const float inv_ppr = 1.0f / (float)pieces_per_row;
+    uint4 xv[kMaxPieces];
+    int rowv[kMaxPieces], colv[kMaxPieces];
+#pragma unroll
+    for (int i = 0; i < kMaxPieces; ++i) {
+        const int idx = i * 1024 + tid;
+        rowv[i] = (int)(((float)idx + 0.5f) * inv_ppr);
+        colv[i] = idx - rowv[i] * pieces_per_row;
+        xv[i] = make_uint4(0, 0, 0, 0);
+        if (rowv[i] < 16 && rowv[i] < a.rows)
+            xv[i] = *reinterpret_cast<const uint4*>(a.x + rowv[i] * K + k0 + 8 * colv[i]);
+    }
+    const int64_t wn = min(n0 + 16 * cb + r16, a.columns - 1);  // clamped: never stored
+    const uint8_t* wrow = reinterpret_cast<const uint8_t*>(a.w) + wn * K + k0 + (int64_t)kq * (KS / 4);
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    v4u wv[kMaxSteps];
+#pragma unroll
+    for (int j = 0; j < kMaxSteps; ++j) {
+        const int st = j < steps ? j : steps - 1;
+        wv[j] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wrow + 64 * st + 16 * g));
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxPieces; ++i)
+        if (rowv[i] < 16) *reinterpret_cast<uint4*>(sx + rowv[i] * RS + colv[i] * 16) = xv[i];
+    __syncthreads();
+    v4f_t acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < kMaxSteps; ++j) {
+        if (j >= steps) break;  // uniform
+        v2h h[8];
+        i8x4_to_f16x4(wv[j].x, h[0], h[1]);
+        i8x4_to_f16x4(wv[j].y, h[2], h[3]);
+        i8x4_to_f16x4(wv[j].z, h[4], h[5]);
+        i8x4_to_f16x4(wv[j].w, h[6], h[7]);
+        const v8h b0 = v8h{h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
+        const v8h b1 = v8h{h[4][0], h[4][1], h[5][0], h[5][1], h[6][0], h[6][1], h[7][0], h[7][1]};
+        const uint8_t* px = sx + r16 * RS + (kq * (KS / 4) + 64 * j + 16 * g) * 2;
+        v8h a0, a1;
+        __builtin_memcpy(&a0, px, 16);
+        __builtin_memcpy(&a1, px + 16, 16);
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b0, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b1, acc1, 0, 0, 0);
+    }
+    __syncthreads();  // every wave is done with x; its LDS now holds the partials
+    float* s_part = reinterpret_cast<float*>(sx);  // [16 waves][256]
+    // 16 x 16 accumulator layout: lane holds column lane % 16, rows 4 (lane / 16) .. +3.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s_part[wave * 256 + (4 * g + r) * 16 + r16] = acc0[r] + acc1[r];
+    __syncthreads();
+    {
+        const int c4 = tid >> 8, within = tid & 255;  // column block, (row, column) in it
+        const int64_t m = within >> 4, n = n0 + 16 * c4 + (within & 15);
+        if (m < a.rows && n < a.columns) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) sum += s_part[(4 * q + c4) * 256 + within];
+            a.partial[((int64_t)sp * a.rows + m) * a.columns + n] = sum;
+        }
+    }
+}
+
+hipError_t launch_skinny_split(const W8A16Args& a, int splits, hipStream_t stream);
+int cu_count();
+
+// Split count for the split-K skinny kernel (1: not split): rows <= 16, int8
+// weights, K / splits a multiple of 256 and at most 1024, and the partial
+// sums fit the workspace. By default it splits only where the unsplit
+// LDS-staged kernel (16 columns per workgroup, K <= 4096) needs more than one
+// round of workgroups: measured on MI355X, 16 x 4096 -> 14336 21.7 us split
+// four ways against 25.7, 16 x 2048 -> 8192 9.4 against 10.5, but config 1
+// (16 x 4096 -> 4096, one round) 9.6 against 7.8: a single round is bound by
+// the cold fetch of x and the first weight latency, not by the x traffic the
+// split saves, and the reduction launch adds ~1.5 us.
+// OMNI_W8A16_SKINNY_SPLIT=<n> pins n (0: off; test aid, read on every call).
+int skinny_splits(int64_t rows, int64_t width, int64_t columns, int64_t partial_elems, int cus) {
+    if (rows > 16 || width % 256 != 0) return 1;
+    const char* v = std::getenv("OMNI_W8A16_SKINNY_SPLIT");
+    int want = v ? std::atoi(v) : -1;
+    if (want == 0) return 1;
+    if (want < 0) {
+        if (width > kSkinnyLdsMaxK || columns <= 16LL * cus) return 1;
+        want = 1;
+        while (width / want > kSkinnySplitMaxKS) want *= 2;
+    }
+    if (want < 2 || width % (256LL * want) != 0 || width / want > kSkinnySplitMaxKS) return 1;
+    if (want * rows * columns > partial_elems) return 1;
+    return want;
+}
+
 // OMNI_W8A16_SKINNY=1 keeps 5..16-row calls on w8a16_skinny_kernel instead
 // of the LDS-staged kernel (test aid; read on every call).
 int skinny_route() {
@@ -621,6 +742,10 @@ hipError_t launch_skinny_cfg(const W8A16Args& a, hipStream_t stream) {
 template <int WB>
 hipError_t launch_skinny(const W8A16Args& a, hipStream_t stream) {
     if (a.rows == 0 || a.columns == 0) return hipSuccess;
+    if constexpr (WB == 8) {
+        const int sp = skinny_splits(a.rows, a.width, a.columns, a.partial ? a.partial_elems : 0, cu_count());
+        if (sp > 1) return launch_skinny_split(a, sp, stream);
+    }
     if (a.rows <= 16 && a.width % 64 == 0 && a.width <= kSkinnyLdsMaxK && skinny_route() != 1) {
         hipLaunchKernelGGL((w8a16_skinny_lds_kernel<WB>), dim3((unsigned)((a.columns + 15) / 16)), dim3(1024), 0,
                            stream, a);
@@ -1442,6 +1567,17 @@ __global__ __launch_bounds__(256) void w8a16_split_reduce_kernel(W8A16Args a, in
     }
 }
 
+hipError_t launch_skinny_split(const W8A16Args& a, int splits, hipStream_t stream) {
+    const int64_t units = ((a.columns + 63) / 64) * splits;
+    hipLaunchKernelGGL(w8a16_skinny_split_kernel, dim3((unsigned)units), dim3(1024), 0, stream, a, splits);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t quads = (a.rows * a.columns + 3) / 4;
+    hipLaunchKernelGGL(w8a16_split_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, a,
+                       splits);
+    return hipGetLastError();
+}
+
 int cu_count() {
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -1595,6 +1731,12 @@ W16Plan plan_w8a16(const W8A16Args& a, int cus, bool ws_limited) {
     // for 128 x 256), else 128 x 256.
     if (tiles64 <= 3 * (int64_t)cus) return with_splits(12);
     return with_splits(16);
+}
+
+int64_t w8a16_skinny_partial_elems(int64_t rows, int64_t columns, int64_t width) {
+    if (rows <= 0 || columns <= 0) return 0;
+    const int sp = skinny_splits(rows, width, columns, INT64_MAX, cu_count());
+    return sp > 1 ? (int64_t)sp * rows * columns : 0;
 }
 
 int64_t w8a16_partial_elems(int64_t rows, int64_t columns, int64_t width) {

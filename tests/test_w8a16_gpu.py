@@ -265,3 +265,41 @@ def test_split_k_workspace_contract(monkeypatch):
     st = L.omni_w8a16_gemm_ws(xd.data_ptr(), wd.data_ptr(), sd.data_ptr(), bd.data_ptr(), rows, columns, width,
                               outs[0].data_ptr(), bad.data_ptr() + 4, 512, stream)
     assert st == _lib.OMNI_BAD_ARGUMENT
+
+
+@pytest.mark.parametrize("splits", ["auto", "2", "4", "8"])
+@pytest.mark.parametrize("rows,width,columns,bias", [(16, 4096, 4096, False), (9, 2048, 1000, True),
+                                                     (5, 8192, 300, True), (12, 256, 70, False),
+                                                     (16, 1024, 4099, True), (13, 12288, 128, False)])
+def test_skinny_split_k(oracle, monkeypatch, splits, rows, width, columns, bias):
+    # The decode-shaped split-K kernel (5..16 rows): units of 64 columns x
+    # K / splits, f32 partial sums, then the in-order reduction. Splits that
+    # do not divide K into multiples of 256 of at most 1024 fall back to the
+    # unsplit kernels; ragged columns, bias, K from 256 to 12288.
+    if splits != "auto":
+        monkeypatch.setenv("OMNI_W8A16_SKINNY_SPLIT", splits)
+    rng = np.random.default_rng(rows * 7 + width + columns + (0 if splits == "auto" else int(splits)))
+    x, w, s, b = make(rng, rows, width, columns, bias=bias)
+    xd, wd, sd, bd = dev(x), dev(w), dev(s), None if b is None else dev(b)
+    got = oi.w8a16_linear(xd, wd, sd, bd)
+    again = oi.w8a16_linear(xd, wd, sd, bd)
+    ref = gpu_f64_reference(x, w, s, b)
+    assert tolerance.rel_err(host(got), ref) <= tolerance.FP16_REL_TOL, (splits, rows, width, columns)
+    assert torch.equal(got, again)
+    monkeypatch.setenv("OMNI_W8A16_SKINNY_SPLIT", "0")
+    plain = oi.w8a16_linear(xd, wd, sd, bd)
+    assert tolerance.rel_err(host(plain), ref) <= tolerance.FP16_REL_TOL
+
+
+def test_skinny_split_k_workspace_size():
+    from omni_int8 import _lib
+    L = _lib.lib()
+    # split where the unsplit kernel needs more than one round of 16-column
+    # workgroups (N > 16 x 256 CUs), K <= 4096
+    assert L.omni_w8a16_gemm_workspace_size(16, 14336, 4096) == 4 * 16 * 14336 * 4
+    assert L.omni_w8a16_gemm_workspace_size(16, 8192, 2048) == 2 * 16 * 8192 * 4
+    assert L.omni_w8a16_gemm_workspace_size(16, 4096, 4096) == 0                   # config 1: one round
+    assert L.omni_w8a16_gemm_workspace_size(16, 8192, 1024) == 0                   # K fits one unit
+    assert L.omni_w8a16_gemm_workspace_size(16, 8192, 4160) == 0                   # K % 256 != 0
+    assert L.omni_w8a16_gemm_workspace_size(16, 8192, 8192) == 0                   # K > 4096
+    assert L.omni_w8a16_gemm_workspace_size(17, 14336, 4096) == 0                  # skinny, not split
