@@ -1559,12 +1559,19 @@ __global__ __launch_bounds__(256) void w8a16_split_reduce_kernel(W8A16Args a, in
         }
     }
     int64_t c = i % a.columns;
+    _Float16 o[4];
     for (int e = 0; e < e_end; ++e) {
         if (e > 0 && ++c == a.columns) c = 0;
         const float sc = (float)a.scale[c];
         const float bi = a.bias ? (float)a.bias[c] : 0.0f;
-        a.out[i + e] = (_Float16)(v[e] * sc + bi);
+        o[e] = (_Float16)(v[e] * sc + bi);
     }
+    if (e_end == 4 && reinterpret_cast<uintptr_t>(a.out + i) % 8 == 0) {
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        *reinterpret_cast<h4*>(a.out + i) = h4{o[0], o[1], o[2], o[3]};
+        return;
+    }
+    for (int e = 0; e < e_end; ++e) a.out[i + e] = o[e];
 }
 
 hipError_t launch_skinny_split(const W8A16Args& a, int splits, hipStream_t stream) {

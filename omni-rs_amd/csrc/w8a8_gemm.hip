@@ -1248,17 +1248,37 @@ __global__ __launch_bounds__(256) void w8a8_split_reduce_kernel(W8A8Args a, int 
     }
     const bool has_zero = a.w_zero != nullptr;
     int64_t row = i / a.columns, col = i - row * a.columns;
+    float o[4];
     for (int e = 0; e < e_end; ++e) {
-        const int64_t idx = i + e;
         if (e > 0 && ++col == a.columns) col = 0, ++row;
         const unsigned prod = has_zero ? (unsigned)a.x_sum[row] * (unsigned)a.w_zero[col] : 0u;
         const int centered = (int)(v[e] - prod);
-        const float o = w8a8_scale(centered, a.x_scale[row], a.w_scale[col], a.bias ? a.bias[col] : -0.0f);
-        if constexpr (DUMP) a.acc_dump[idx] = (int)v[e];
+        o[e] = w8a8_scale(centered, a.x_scale[row], a.w_scale[col], a.bias ? a.bias[col] : -0.0f);
+    }
+    // Whole 16-byte (8-byte) stores when aligned: four 4-byte nontemporal
+    // stores into one line were written back to HBM separately.
+    const uintptr_t oaddr = reinterpret_cast<uintptr_t>(a.out) + (uintptr_t)i * (OUT16 ? 2 : 4);
+    const bool vec = e_end == 4 && oaddr % (OUT16 ? 8 : 16) == 0 &&
+                     (!DUMP || reinterpret_cast<uintptr_t>(a.acc_dump + i) % 16 == 0);
+    if (vec) {
+        if constexpr (DUMP)
+            *reinterpret_cast<int4*>(a.acc_dump + i) = make_int4((int)v[0], (int)v[1], (int)v[2], (int)v[3]);
+        if constexpr (OUT16) {
+            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+            stream_store(reinterpret_cast<h4*>(static_cast<_Float16*>(a.out) + i),
+                         h4{(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]});
+        } else {
+            typedef float f4 __attribute__((ext_vector_type(4)));
+            stream_store(reinterpret_cast<f4*>(static_cast<float*>(a.out) + i), f4{o[0], o[1], o[2], o[3]});
+        }
+        return;
+    }
+    for (int e = 0; e < e_end; ++e) {
+        if constexpr (DUMP) a.acc_dump[i + e] = (int)v[e];
         if constexpr (OUT16)
-            stream_store(static_cast<_Float16*>(a.out) + idx, (_Float16)o);
+            stream_store(static_cast<_Float16*>(a.out) + i + e, (_Float16)o[e]);
         else
-            stream_store(static_cast<float*>(a.out) + idx, o);
+            stream_store(static_cast<float*>(a.out) + i + e, o[e]);
     }
 }
 
@@ -1378,19 +1398,20 @@ int w8a8_split_override() {
     return v ? std::atoi(v) : 0;
 }
 
-// Split K when 256 x 128 tiles fill at most half of the CUs and K is long
-// (>= 8192): K split up to 6 ways, at most one unit per CU, on the 256 x 128
-// pair ring. The partial sums cost one int32 write and read per element and
-// split, so shorter K does not pay (MI355X, the reference's shapes: 256 x
-// 4096 x 12288 70 -> 32 us, 256 x 3072 x 12288 69 -> 29 us, 512 x 4096 x
-// 12288 68 -> 49 us; at K = 4096 a split gains at most 6 % and 256 x 12288 x
-// 4096 loses 28 -> 41 us).
+// Split K when 256 x 128 tiles fill at most half of the CUs and K >= 8192,
+// or at most an eighth of them and K >= 4096: K split up to 6 ways, at most
+// one unit per CU, on the 256 x 128 pair ring. The partial sums cost one
+// int32 write and read per element and split, so shorter K, or more tiles,
+// do not pay (MI355X, the reference's shapes: 256 x 4096 x 12288 69 -> 29
+// us, 256 x 3072 x 12288 69 -> 27 us, 512 x 4096 x 12288 69 -> 40 us,
+// 256 x 4096 x 4096 24.7 -> 22.8 us; 512 x 4096 x 4096 26.2 unsplit against
+// 26.6 at best split, 256 x 12288 x 4096 27.8 against 32.5).
 int w8a8_auto_splits(int64_t rows, int64_t columns, int64_t width, int64_t cus) {
     const int ov = w8a8_split_override();
     if (ov > 1) return ov;
-    if (width % 64 != 0 || width < 8192) return 1;
+    if (width % 64 != 0 || width < 4096) return 1;
     const int64_t tiles = ((rows + 255) / 256) * ((columns + 127) / 128);
-    if (2 * tiles > cus) return 1;
+    if (width >= 8192 ? 2 * tiles > cus : 8 * tiles > cus) return 1;
     const int64_t want = cus / tiles;
     return (int)(want > 6 ? 6 : want);
 }

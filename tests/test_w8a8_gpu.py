@@ -540,15 +540,16 @@ def test_w8a8_split_k_bit_identical(oracle, splits, monkeypatch):
 
 
 def test_w8a8_split_k_workspace_contract(monkeypatch):
-    # omni_w8a8_gemm_workspace_size: the reference's 256-row benchmark shape
-    # with K = 12288 splits, its K = 4096 ones and the north-star shapes do
-    # not; omni_w8a8_gemm_ws splits less with a smaller workspace and not at
-    # all with none, bit-identically.
+    # omni_w8a8_gemm_workspace_size: the reference's 256-row benchmark shapes
+    # with 32 tiles split, 256 x 12288 x 4096 (96 tiles) and the north-star
+    # shapes do not; omni_w8a8_gemm_ws splits less with a smaller workspace
+    # and not at all with none, bit-identically.
     from omni_int8 import _lib
     L = _lib.lib()
-    size = L.omni_w8a8_gemm_workspace_size(256, 4096, 12288)
-    assert size >= 2 * 256 * 4096 * 4 and size % (256 * 4096 * 4) == 0, size
-    for m, n, k in ((256, 4096, 4096), (256, 12288, 4096), (4096, 12288, 3072), (4096, 3072, 12288)):
+    for m, n, k in ((256, 4096, 12288), (256, 4096, 4096)):
+        size = L.omni_w8a8_gemm_workspace_size(m, n, k)
+        assert size >= 2 * m * n * 4 and size % (m * n * 4) == 0, (m, n, k, size)
+    for m, n, k in ((256, 12288, 4096), (512, 4096, 4096), (4096, 12288, 3072), (4096, 3072, 12288)):
         assert L.omni_w8a8_gemm_workspace_size(m, n, k) == 0, (m, n, k)
     rows, width, columns = 256, 8192, 1024
     rng = np.random.default_rng(91)
