@@ -147,10 +147,14 @@ inline DeviceTensor w8a16_linear(const DeviceTensor& x, const DeviceTensor& w,
         (bias && (bias->dtype != DType::F16 || bias->numel() != w.dim(0))))
         throw Int8Error(OMNI_BAD_ARGUMENT, "w8a16_linear: shapes/dtypes disagree");
     DeviceTensor out{alloc.allocate((size_t)(x.dim(0) * w.dim(0)) * 2, stream), {x.dim(0), w.dim(0)}, DType::F16};
-    const int st = omni_w8a16_gemm(static_cast<const uint16_t*>(x.data), static_cast<const int8_t*>(w.data),
-                                   static_cast<const uint16_t*>(scale.data),
-                                   bias ? static_cast<const uint16_t*>(bias->data) : nullptr, x.dim(0),
-                                   w.dim(0), x.dim(1), static_cast<uint16_t*>(out.data), stream);
+    // Split-K partial sums when the shape asks for them (0 bytes: none).
+    const size_t ws_bytes = omni_w8a16_gemm_workspace_size(x.dim(0), w.dim(0), x.dim(1));
+    void* ws = ws_bytes ? alloc.allocate(ws_bytes, stream) : nullptr;
+    const int st = omni_w8a16_gemm_ws(static_cast<const uint16_t*>(x.data), static_cast<const int8_t*>(w.data),
+                                      static_cast<const uint16_t*>(scale.data),
+                                      bias ? static_cast<const uint16_t*>(bias->data) : nullptr, x.dim(0),
+                                      w.dim(0), x.dim(1), static_cast<uint16_t*>(out.data), ws, ws_bytes, stream);
+    if (ws) alloc.release(ws, stream);
     if (st != OMNI_OK) {
         alloc.release(out.data, stream);
         if (st == OMNI_NOT_HANDLED) throw Int8Error(st, omni_int8_last_error());

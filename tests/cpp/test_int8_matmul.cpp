@@ -147,8 +147,11 @@ static void shape_mismatch_returns_none() {
 static void w8a16_linear_matches_ground_truth() {
     std::puts("w8a16_linear_matches_ground_truth");
     omni_kernel::HipAllocator alloc;
-    for (int64_t rows : {1, 4, 37}) {
-        const int64_t width = 512, columns = 96;
+    // The last two shapes split K through the workspace (the GEMM, and the
+    // 5..16-row kernel when its 16-column units need more than one round).
+    const int64_t cases[][3] = {{1, 512, 96}, {4, 512, 96}, {37, 512, 96}, {200, 8192, 160}, {16, 2048, 4200}};
+    for (const auto& cs : cases) {
+        const int64_t rows = cs[0], width = cs[1], columns = cs[2];
         std::vector<uint16_t> x(rows * width), scale(columns), bias(columns);
         std::vector<int8_t> w(columns * width);
         uint64_t st = 0x9e3779b97f4a7c15ull;
