@@ -1848,8 +1848,8 @@ hipError_t launch_f16_skinny(const W8A16Args& a, hipStream_t stream) { return la
 // OMNI_F16_TILE=<n> pins the fp16 GEMM kernel (tuning and test aid):
 // 1 = tiled 128 x 128, 2 = tiled 64 x 64, 4/5/6 = ring 256 x 128 / 128 x 128 /
 // 128 x 256, 7/8 = ring 256 x 256 / 256 x 128 on 32-element K tiles, 10 =
-// eight-wave ring 256 x 128, 12 = eight-wave ring 256 x 256 on 32-element K
-// tiles (rings: K % 64 == 0 only). Read on every call.
+// eight-wave ring 256 x 128, 12 / 13 = eight-wave ring 256 x 256 on 32- /
+// 64-element K tiles (rings: K % 64 == 0 only). Read on every call.
 hipError_t launch_f16_mfma(const W8A16Args& a, hipStream_t stream) {
     if (a.rows == 0 || a.columns == 0) return hipSuccess;
     const bool ring_ok = ring16_fits(a);
@@ -1864,25 +1864,27 @@ hipError_t launch_f16_mfma(const W8A16Args& a, hipStream_t stream) {
         case 8: if (ring_ok) return launch_ring16_cfg<256, 128, 16, 2, 3, 1>(a, stream); break;
         case 10: if (ring_ok) return launch_ring16_cfg<256, 128, 16, 4, 3, 2, 1, 8>(a, stream); break;
         case 12: if (ring_ok) return launch_ring16_cfg<256, 256, 16, 4, 3, 1, 1, 8>(a, stream); break;
+        case 13: if (ring_ok) return launch_ring16_cfg<256, 256, 16, 4, 2, 2, 1, 8>(a, stream); break;
         default: break;
     }
     const int64_t cus = cu_count();
-    // Eight-wave rings (two waves per SIMD): 256 x 256 tiles on 32-element K
-    // tiles (each wave 64 x 128) or 256 x 128 tiles on 64-element K tiles
-    // (each wave 64 x 64), whichever a rounds cost model picks: tiles run in
-    // rounds of one per CU, a partial last round with fill f costs 0.7 +
-    // 0.3 f of a full one, and a 256 x 256 tile costs 1.93 times a 256 x 128
-    // one (MI355X, 4096 x 4096 x 12288: 359.6 / 373.4 us, against 401 for
-    // the four-wave 256 x 256 ring and 319 for torch.matmul; 2048 x 4096 x
-    // 4096: 65.6 us for 256 x 128 against 67.3 for torch.matmul; 4352 x
-    // 4096 x 12288: 426.8 against 422.9).
+    // Eight-wave rings (two waves per SIMD, each 64 x 128 or 64 x 64) on
+    // 64-element K tiles (whole 128-byte lines of x and W): 256 x 256 tiles
+    // in a 2-stage ring or 256 x 128 tiles in a 3-stage ring, whichever a
+    // rounds cost model picks: tiles run in rounds of one per CU, a partial
+    // last round with fill f costs 0.7 + 0.3 f of a full one, and a 256 x 256
+    // tile costs 1.80 times a 256 x 128 one (MI355X, best of three:
+    // 4096 x 4096 x 12288 334.5 / 365.0 us, torch.matmul 321.0; 4352 x 4096 x
+    // 12288 408.1 / 422.8, torch.matmul 418.7; 2048 x 4096 x 4096 80.4 /
+    // 64.6, torch.matmul 62.5; the 256 x 256 ring on 32-element K tiles
+    // 356.9 / 433.7 / 79.4).
     if (ring_ok && a.width >= 3072) {
         auto rounds = [&](int64_t bn) {
             const int64_t tiles = ((a.rows + 255) / 256) * ((a.columns + bn - 1) / bn);
             const int64_t full = tiles / cus, rem = tiles % cus;
             return (double)full + (rem ? 0.7 + 0.3 * (double)rem / (double)cus : 0.0);
         };
-        if (1.93 * rounds(256) <= rounds(128)) return launch_ring16_cfg<256, 256, 16, 4, 3, 1, 1, 8>(a, stream);
+        if (1.80 * rounds(256) <= rounds(128)) return launch_ring16_cfg<256, 256, 16, 4, 2, 2, 1, 8>(a, stream);
         return launch_ring16_cfg<256, 128, 16, 4, 3, 2, 1, 8>(a, stream);
     }
     const int64_t big_tiles = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
