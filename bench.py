@@ -298,10 +298,32 @@ def w4a16_bench(torch, oi, gen, dev, stream, steps):
     t = timed_graph(g, stream) / iters
     del g
     nbytes = wbytes + 2 * M * K + 2 * M * N
-    return {"M": M, "K": K, "N": N, "group": 128, "weight_copies": copies,
-            "us_per_launch": round(t * 1e6, 3), "GB/s": round(nbytes / t / 1e9, 1),
-            "roofline_frac": round(nbytes / t / 1e9 / PEAK_HBM_GBS, 4),
-            "traffic": row_traffic("w4a16_gemv")}
+    res = {"M": M, "K": K, "N": N, "group": 128, "weight_copies": copies,
+           "us_per_launch": round(t * 1e6, 3), "GB/s": round(nbytes / t / 1e9, 1),
+           "roofline_frac": round(nbytes / t / 1e9 / PEAK_HBM_GBS, 4),
+           "traffic": row_traffic("w4a16_gemv")}
+    # The same weights at prefill (M=1024): the fp16-MFMA ring GEMM, packed
+    # codes staged in LDS and dequantised to f16(q * s) in registers, in TFLOP/s.
+    Mp = 1024
+    xp = torch.randn((Mp, K), generator=gen, device=dev).half()
+
+    def prefill():
+        i = idx[0] % copies
+        oi.w4a16_linear(xp, ws[i], ss[i])
+        idx[0] += 1
+
+    mark(torch, "w4a16_prefill")
+    for _ in range(3):
+        prefill()
+    iters = max(copies, steps)
+    g = graph_of(prefill, iters)
+    tp = timed_graph(g, stream) / iters
+    del g
+    flops = 2.0 * Mp * N * K
+    res["prefill"] = {"M": Mp, "K": K, "N": N, "us": round(tp * 1e6, 2),
+                      "TFLOP/s": round(flops / tp / 1e12, 1),
+                      "roofline_frac": round(flops / tp / 1e12 / PEAK_F16_TFLOPS, 4)}
+    return res
 
 
 def f16_bench(torch, gen, dev, stream, steps):

@@ -189,6 +189,14 @@ __device__ __forceinline__ void lds_copy16_saddr(unsigned voff, const void* base
 #endif
 }
 
+// The same for 4 bytes per lane: lane l's dword lands at lds_byte + 4 l.
+__device__ __forceinline__ void lds_copy4_saddr(unsigned voff, const void* base, unsigned lds_byte) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds_byte)
+                 : "memory", "m0");
+#endif
+}
+
 // LDS byte address of a __shared__ object, as a wave-uniform integer.
 __device__ __forceinline__ unsigned lds_addr(const void* p) {
 #if defined(__HIP_DEVICE_COMPILE__)

@@ -64,14 +64,19 @@ __device__ __forceinline__ void i8x4_to_f16x4_biased(u32 word, v2h& lo, v2h& hi)
 // crates/minicpm-v/src/quant.rs:22-29 unpacks them) -> four f16 pairs in k
 // order (n0,n1) (n2,n3) (n4,n5) (n6,n7), exact: bytes [n, 0x64] are the f16
 // 1024 + n, and one packed subtract of 1032 leaves n - 8.
+// Byte t of word >> 4 holds code 2t + 1 in its low nibble: two v_perm_b32
+// and two masks give the codes in k order one per byte, and one v_perm_b32
+// per pair spreads two of them under 0x64 bytes (nine integer ops per word).
 __device__ __forceinline__ void i4x8_to_f16x8(u32 word, v2h (&h)[4]) {
-    const u32 lo = word & 0x0F0F0F0Fu;         // n0 n2 n4 n6
-    const u32 hi = (word >> 4) & 0x0F0F0F0Fu;  // n1 n3 n5 n7
+    const u32 sh = word >> 4;
+    const u32 c0 = __builtin_amdgcn_perm(sh, word, 0x05010400u) & 0x0F0F0F0Fu;  // n0 n1 n2 n3
+    const u32 c1 = __builtin_amdgcn_perm(sh, word, 0x07030602u) & 0x0F0F0F0Fu;  // n4 n5 n6 n7
+    const u32 k64 = 0x64646464u;
     const v2h k1032 = {(_Float16)1032.0f, (_Float16)1032.0f};
-    h[0] = bits_half2(__builtin_amdgcn_perm(hi, lo, 0x0C040C00u) | 0x64006400u) - k1032;
-    h[1] = bits_half2(__builtin_amdgcn_perm(hi, lo, 0x0C050C01u) | 0x64006400u) - k1032;
-    h[2] = bits_half2(__builtin_amdgcn_perm(hi, lo, 0x0C060C02u) | 0x64006400u) - k1032;
-    h[3] = bits_half2(__builtin_amdgcn_perm(hi, lo, 0x0C070C03u) | 0x64006400u) - k1032;
+    h[0] = bits_half2(__builtin_amdgcn_perm(k64, c0, 0x04010400u)) - k1032;
+    h[1] = bits_half2(__builtin_amdgcn_perm(k64, c0, 0x04030402u)) - k1032;
+    h[2] = bits_half2(__builtin_amdgcn_perm(k64, c1, 0x04010400u)) - k1032;
+    h[3] = bits_half2(__builtin_amdgcn_perm(k64, c1, 0x04030402u)) - k1032;
 }
 
 // Eight int4 codes of `word` as the f16 values 1024 + nibble (exact), one
@@ -1177,22 +1182,42 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a16_mfma_kernel(W
 //
 // NW = 8: eight waves (two per SIMD) share the ring, each owning half as
 // many accumulators, so one wave's MFMAs can issue while the other waits.
+//
+// WB = 4 (W4A16, packed int4 codes plus 8, low nibble first, bf16 scales per
+// group of `group` values along K, group % 64 == 0): a K tile's 64 codes are
+// 32 bytes per weight row, so one 64-byte stage row holds two weight rows
+// (logical chunks 0, 1: the even row's bytes 0..15, 16..31; 2, 3: the odd
+// row's), copied with the same swizzle. A lane's 16 codes of a pair are one
+// 8-byte read; they become f16(q * s) (nibble as 1024 + n, minus 1032, times
+// the group scale in f16), four codes at a time spread over the MFMA slots
+// of the pair before the one that uses them, so the conversion overlaps the
+// MFMAs. The scales ride in the ring too: behind each stage's
+// rows, the aligned bf16 pair holding the tile's group for every column (one
+// 4-byte-per-lane copy per wave per K tile, 64 columns each).
 template <int BM, int BN, int WB = 8, int WMW = 2, int S = 3, int KP = 2, int OCC = 1, bool SK = false, int NW = 4>
 __global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, int splits) {
     static_assert(S == 2 || S == 3, "2 or 3 stages");
     static_assert(KP == 2 || (KP == 1 && WB == 16), "32-element K tiles need f16 weights");
+    static_assert(WB == 4 || WB == 8 || WB == 16, "int4, int8 or f16 weights");
     constexpr int WNW = NW / WMW;             // waves along N
     constexpr int WM = BM / WMW, WN = BN / WNW;
     constexpr int FM = WM / 32, FN = WN / 32;
-    constexpr int kWH = WB / 8;               // 64-byte W rows per column per 64 K
+    constexpr int kWH = WB == 16 ? 2 : 1;     // 64-byte W rows per column per 64 K (int4: half of one)
     constexpr int kXR = KP;                   // 64-byte x rows per row per K tile
     constexpr int kWR = KP == 2 ? kWH : 1;    // 64-byte W rows per column per K tile
-    constexpr int kRows = kXR * BM + kWR * BN;  // 64-byte stage rows: x k 0..31 (, x k 32..63), W
-    constexpr int kStage = kRows * 64;
+    constexpr int kWRows = WB == 4 ? BN / 2 : kWR * BN;  // W stage rows per K tile
+    constexpr int kWBytes = 32 * KP * WB / 8;  // bytes of a W row per K tile
+    constexpr int kRows = kXR * BM + kWRows;  // 64-byte stage rows: x k 0..31 (, x k 32..63), W
+    constexpr int kScOff = kRows * 64;        // int4: scale dwords [BN] behind the rows
+    constexpr int kStage = kRows * 64 + (WB == 4 ? BN * 4 : 0);
     constexpr int kCpw = kRows / (16 * NW);   // 1 KiB copies per wave per K tile
+    constexpr int kOps = kCpw + (WB == 4 ? 1 : 0);  // vector-memory ops per wave per K tile
     constexpr int kFrags = 2 * FM + kWH * FN; // fragment reads per pair
     static_assert(kRows % (16 * NW) == 0 && FM >= 1 && FN >= 1 && WMW * WNW == NW, "tile shape");
     static_assert(kCpw <= 2 * FM * FN && kFrags <= 2 * FM * FN, "one read and copy per MFMA slot");
+    static_assert((S - 1) * kOps < 64, "ops in flight within vmcnt");
+    static_assert(WB != 4 || (KP == 2 && FM >= 2 && BN % 64 == 0), "int4 ring shape");
+    constexpr int FN4 = WB == 4 ? FN : 1;
     static_assert(S * kStage + 4 * BN * 4 <= 160 * 1024 / OCC, "LDS");
     __shared__ __attribute__((aligned(1024))) uint8_t st0[kStage];
     __shared__ __attribute__((aligned(1024))) uint8_t st1[kStage];
@@ -1223,6 +1248,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, i
     const int cp_row = lane >> 2;
     const int cp_chunk = (lane & 3) ^ ((lane >> 4) & 3);
     unsigned voff[kCpw];
+    unsigned voff_sc = 0;  // int4: this lane's scale column, byte offset of its row
     int64_t m0 = 0, n0 = 0;
     float p_sc = 0.0f, p_bi = 0.0f;
     auto tile_origin = [&](int u, int64_t& tm0, int64_t& tn0) {
@@ -1265,12 +1291,21 @@ __global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, i
                 const int half = c16 >= BM;
                 const int64_t row = min(m0 + (c16 - half * BM) + cp_row, a.rows - 1);
                 voff[j] = (unsigned)(row * K * 2) + half * 64 + cp_chunk * 16;
+            } else if constexpr (WB == 4) {
+                // stage row rel + cp_row holds weight rows 2 (rel + cp_row) and +1
+                const int rel = c16 - kXR * BM;
+                const int64_t row = min(n0 + 2 * (rel + cp_row) + (cp_chunk >> 1), a.columns - 1);
+                voff[j] = (unsigned)(row * (K / 2)) + (cp_chunk & 1) * 16;
             } else {
                 const int rel = c16 - kXR * BM;
                 const int half = WB == 16 && rel >= BN;
                 const int64_t row = min(n0 + (rel - half * BN) + cp_row, a.columns - 1);
                 voff[j] = (unsigned)(row * K * kWH) + half * 64 + cp_chunk * 16;
             }
+        }
+        if constexpr (WB == 4) {
+            const int64_t col = min(n0 + (wave % (BN / 64)) * 64 + lane, a.columns - 1);
+            voff_sc = (unsigned)(col * (K / a.group) * 2);
         }
     };
     auto load_params = [&](int64_t pn0) {
@@ -1293,13 +1328,22 @@ __global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, i
             ktiles = min(kts, ktiles_all - kbase);
         }
     };
+    // int4: group of K tile kk (a scale pair holds groups 2i, 2i + 1).
+    const int gdiv = WB == 4 ? (int)(a.group / 64) : 1;
     auto copy_one = [&](int kt, int s, int j) {
         const int64_t kk = kbase + min(kt, ktiles - 1);
         const int c = slot(j);
         const bool is_x = c * 16 < kXR * BM;  // wave-uniform
         const uint8_t* base = is_x ? reinterpret_cast<const uint8_t*>(a.x) + kk * 64 * KP
-                                   : reinterpret_cast<const uint8_t*>(a.w) + kk * 32 * KP * kWH;
+                                   : reinterpret_cast<const uint8_t*>(a.w) + kk * kWBytes;
         lds_copy16_saddr(voff[j], base, stage_lds[s] + c * 1024);
+        if constexpr (WB == 4) {
+            if (j == kCpw - 1) {
+                const int g = (int)kk / gdiv;
+                lds_copy4_saddr(voff_sc, a.gscale + (g & ~1),
+                                stage_lds[s] + kScOff + (wave % (BN / 64)) * 256);
+            }
+        }
     };
     auto copy_tile = [&](int kt, int s) {
 #pragma unroll
@@ -1313,11 +1357,33 @@ __global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, i
     auto offB16 = [&](int p, int j) {
         return (kXR * BM + p * BN + wn * WN + fr) * 64 + (((2 * fh + j) ^ fq) << 4);
     };
+    // int4: column c = wn WN + fr (+ 32 per block) sits in stage row c / 2,
+    // logical chunk 2 (c % 2) + p, whose swizzle key is (c / 8) % 4.
+    auto offB4 = [&](int p) {
+        return (kXR * BM + (wn * WN + fr) / 2) * 64 + ((((fr & 1) * 2 + p) ^ ((fr >> 3) & 3)) << 4) + 8 * fh;
+    };
     v4i xa0[FM][2], xb0[FN][kWH], xa1[FM][2], xb1[FN][kWH];
+    v8h bh0[FN4][2], bh1[FN4][2];  // int4: converted codes of a pair
+    uint16_t sc[FN4];              // int4: the K tile's bf16 scales (read with pair 0's codes)
     // Fragment idx of a pair: A (i, j) for idx < 2 FM, else B idx - 2 FM
     // (int8: column block idx - 2 FM; f16: block (idx - 2 FM) / 2, half (idx - 2 FM) % 2).
-    auto read_frag = [&](int s, int p, int idx, v4i (&xa)[FM][2], v4i (&xb)[FN][kWH]) {
-        if (idx < 2 * FM) {
+    // int4 reads its B blocks first, idx < FN (with pair 0, the tile's
+    // scales), then A idx - FN; kt is the K tile in stage s.
+    auto read_frag = [&](int s, int p, int idx, v4i (&xa)[FM][2], v4i (&xb)[FN][kWH], int kt) {
+        if constexpr (WB == 4) {
+            if (idx < FN) {
+                const uint2 w2 = *reinterpret_cast<const uint2*>(stage(s) + offB4(p) + idx * 16 * 64);
+                xb[idx][0] = v4i{(int)w2.x, (int)w2.y, 0, 0};
+                if (p == 0) {
+                    const int g = (int)(kbase + kt) / gdiv;
+                    sc[idx] = *reinterpret_cast<const uint16_t*>(stage(s) + kScOff + (wn * WN + 32 * idx + fr) * 4 +
+                                                                 (g & 1) * 2);
+                }
+            } else {
+                const int i = idx - FN;
+                xa[i >> 1][i & 1] = *reinterpret_cast<const v4i*>(stage(s) + offA(p, i & 1) + (i >> 1) * 32 * 64);
+            }
+        } else if (idx < 2 * FM) {
             xa[idx >> 1][idx & 1] =
                 *reinterpret_cast<const v4i*>(stage(s) + offA(p, idx & 1) + (idx >> 1) * 32 * 64);
         } else if constexpr (WB == 8) {
@@ -1332,10 +1398,39 @@ __global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, i
     // are converted first; then the k 0..7 products of all FM x FN blocks run,
     // then the k 8..15 ones, so no MFMA waits for the one just before it (two
     // back-to-back MFMAs into one accumulator would serialise).
+    // int4: piece pc of a pair's conversion, codes 4 (pc % 4) .. +3 of block
+    // pc / 4 (i4x8_to_f16x8's steps, then times the scale), eight VALU ops.
+    auto conv4 = [&](int pc, v4i (&xb)[FN][kWH], v8h (&bh)[FN4][2]) {
+        if constexpr (WB == 4) {
+            const int jn = pc >> 2, w = (pc >> 1) & 1, hc = pc & 1;
+            const u32 word = (u32)xb[jn][0][w];
+            const u32 c = __builtin_amdgcn_perm(word >> 4, word, hc ? 0x07030602u : 0x05010400u) & 0x0F0F0F0Fu;
+            const v2h k1032 = {(_Float16)1032.0f, (_Float16)1032.0f};
+            const _Float16 sh = (_Float16)bf16_to_f32(sc[jn]);  // (converted at first use)
+            const v2h s2 = {sh, sh};
+            const v2h h0 = (bits_half2(__builtin_amdgcn_perm(0x64646464u, c, 0x04010400u)) - k1032) * s2;
+            const v2h h1 = (bits_half2(__builtin_amdgcn_perm(0x64646464u, c, 0x04030402u)) - k1032) * s2;
+            bh[jn][w][4 * hc] = h0[0];
+            bh[jn][w][4 * hc + 1] = h0[1];
+            bh[jn][w][4 * hc + 2] = h1[0];
+            bh[jn][w][4 * hc + 3] = h1[1];
+        }
+    };
+    // After MFMA slot q: the conversion pieces that slot carries, spread
+    // evenly from slot 3 on (block jn's codes are read at slot jn).
+    auto conv_at = [&](int q, v4i (&xb)[FN][kWH], v8h (&bh)[FN4][2]) {
+        if constexpr (WB == 4) {
+            constexpr int ns = 2 * FM * FN, np = 4 * FN, c0 = 3;
+#pragma unroll
+            for (int i = 0; i < np; ++i)
+                if (c0 + i * (ns - c0) / np == q) conv4(i, xb, bh);
+        }
+    };
     v16f acc[FM][FN];
-    auto pair_mfmas = [&](v4i (&xa)[FM][2], v4i (&xb)[FN][kWH], auto&& after) {
+    auto pair_mfmas = [&](v4i (&xa)[FM][2], v4i (&xb)[FN][kWH], const v8h (&bq)[FN4][2], auto&& after) {
         // f16 weights (WB = 16) feed the MFMA straight from their fragment
-        // registers; int8 weights are converted into bh first.
+        // registers; int8 weights are converted into bh first; int4 ones
+        // arrive converted in bq.
         v8h bh[WB == 8 ? FN : 1][2];
         if constexpr (WB == 8) {
 #pragma unroll
@@ -1358,6 +1453,8 @@ __global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, i
                     __builtin_memcpy(&av, &xa[i][half], 16);
                     if constexpr (WB == 8)
                         bv = bh[jn][half];
+                    else if constexpr (WB == 4)
+                        bv = bq[jn][half];
                     else
                         __builtin_memcpy(&bv, &xb[jn][half * (kWH - 1)], 16);
                     acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc[i][jn], 0, 0, 0);
@@ -1392,10 +1489,12 @@ __global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, i
 #pragma unroll
             for (int j = 0; j < FN; ++j) acc[i][j] = v16f{};
 
-        s_waitcnt_vm<(S - 1) * kCpw, true>();
+        s_waitcnt_vm<(S - 1) * kOps, true>();
         lds_barrier();
 #pragma unroll
-        for (int idx = 0; idx < kFrags; ++idx) read_frag(0, 0, idx, xa0, xb0);
+        for (int idx = 0; idx < kFrags; ++idx) read_frag(0, 0, idx, xa0, xb0, 0);
+#pragma unroll
+        for (int pc = 0; pc < 4 * FN4; ++pc) conv4(pc, xb0, bh0);
 
         if constexpr (KP == 2) {
             for (int t0 = 0; t0 < ktiles; t0 += S) {
@@ -1404,15 +1503,17 @@ __global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, i
                     const int kt = t0 + u;
                     if (kt < ktiles) {  // uniform across the workgroup
                         // Pair 0 of tile kt; reads of pair 1.
-                        pair_mfmas(xa0, xb0, [&](int q) {
-                            if (q < kFrags) read_frag(u, 1, q, xa1, xb1);
+                        pair_mfmas(xa0, xb0, bh0, [&](int q) {
+                            if (q < kFrags) read_frag(u, 1, q, xa1, xb1, kt);
+                            conv_at(q, xb1, bh1);
                         });
-                        s_waitcnt_vm<(S - 2) * kCpw, true>();
+                        s_waitcnt_vm<(S - 2) * kOps, true>();
                         lds_barrier();  // tile kt+1 landed everywhere; stage u is read
                         // Pair 1 of tile kt; copies of tile kt+S into stage u; reads of tile kt+1, pair 0.
-                        pair_mfmas(xa1, xb1, [&](int q) {
+                        pair_mfmas(xa1, xb1, bh1, [&](int q) {
                             if (q < kCpw) copy_one(kt + S, u, q);
-                            if (q < kFrags) read_frag((u + 1) % S, 0, q, xa0, xb0);
+                            if (q < kFrags) read_frag((u + 1) % S, 0, q, xa0, xb0, kt + 1);
+                            conv_at(q, xb0, bh0);
                         });
                     }
                 }
@@ -1429,17 +1530,17 @@ __global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, i
                         // Tile kt's fragments were read during tile kt-1: once
                         // tile kt+1 has landed and every wave has passed here,
                         // stage u may be refilled with tile kt+S.
-                        s_waitcnt_vm<(S - 2) * kCpw, true>();
+                        s_waitcnt_vm<(S - 2) * kOps, true>();
                         lds_barrier();
                         if (u2 % 2 == 0) {
-                            pair_mfmas(xa0, xb0, [&](int q) {
+                            pair_mfmas(xa0, xb0, bh0, [&](int q) {
                                 if (q < kCpw) copy_one(kt + S, u, q);
-                                if (q < kFrags) read_frag((u + 1) % S, 0, q, xa1, xb1);
+                                if (q < kFrags) read_frag((u + 1) % S, 0, q, xa1, xb1, kt + 1);
                             });
                         } else {
-                            pair_mfmas(xa1, xb1, [&](int q) {
+                            pair_mfmas(xa1, xb1, bh1, [&](int q) {
                                 if (q < kCpw) copy_one(kt + S, u, q);
-                                if (q < kFrags) read_frag((u + 1) % S, 0, q, xa0, xb0);
+                                if (q < kFrags) read_frag((u + 1) % S, 0, q, xa0, xb0, kt + 1);
                             });
                         }
                     }
@@ -1449,7 +1550,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, i
 
         const int64_t em0 = m0, en0 = n0;
         const int esplit = split;
-        s_waitcnt_vm<(S - 1) * kCpw, true>();
+        s_waitcnt_vm<(S - 1) * kOps, true>();
         lds_barrier();  // every wave is done reading the ring
         if (more) {
             m0 = nm0;
@@ -1823,8 +1924,46 @@ hipError_t launch_w4a16_skinny(const W8A16Args& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// OMNI_W4A16_TILE=<n> pins the W4A16 GEMM kernel (tuning and test aid):
+// 1 / 2 = tiled 128 x 128 / 64 x 64 (codes dequantized through registers),
+// rings 4 / 5 / 6 = 256 x 128 / 128 x 128 / 256 x 256, 10 = 128 x 128 at
+// two workgroups per CU, 16 / 17 = eight-wave 128 x 256 / 256 x 256
+// (rings: K % 64 == 0, group % 64 == 0 and K / group even). Read on every call.
 hipError_t launch_w4a16_mfma(const W8A16Args& a, hipStream_t stream) {
     if (a.rows == 0 || a.columns == 0) return hipSuccess;
+    // (the ring copies a column's scales as aligned bf16 pairs: an even count per row)
+    const bool ring_ok = ring16_fits(a) && a.group % 64 == 0 && (a.width / a.group) % 2 == 0;
+    const char* ov = std::getenv("OMNI_W4A16_TILE");
+    switch (ov ? std::atoi(ov) : 0) {
+        case 1: return launch_mfma16_cfg<128, 128, 64, 2, 2, 4, 4>(a, stream);
+        case 2: return launch_mfma16_cfg<64, 64, 64, 2, 2, 4, 4>(a, stream);
+        case 4: if (ring_ok) return launch_ring16_cfg<256, 128, 4>(a, stream); break;
+        case 5: if (ring_ok) return launch_ring16_cfg<128, 128, 4>(a, stream); break;
+        case 6: if (ring_ok) return launch_ring16_cfg<256, 256, 4>(a, stream); break;
+        case 10: if (ring_ok) return launch_ring16_cfg<128, 128, 4, 2, 3, 2, 2>(a, stream); break;
+        case 16: if (ring_ok) return launch_ring16_cfg<128, 256, 4, 2, 3, 2, 1, 8>(a, stream); break;
+        case 17: if (ring_ok) return launch_ring16_cfg<256, 256, 4, 4, 3, 2, 1, 8>(a, stream); break;
+        default: break;
+    }
+    if (ring_ok) {
+        // Rings 256 x 256 / 256 x 128 / 128 x 128, whichever a rounds cost
+        // model picks: tiles run in rounds of one per CU, a partial last round
+        // with fill f costs 0.7 + 0.3 f of a full one, and a full round costs
+        // c K + e us (MI355X fits over M = 256..4096, K = 3584..18944:
+        // 0.0335 K + 13.6, 0.01435 K + 24.2, 0.0107 K + 8.1).
+        const int64_t cus = cu_count();
+        auto cost = [&](int64_t bm, int64_t bn, double c, double e) {
+            const int64_t tiles = ((a.rows + bm - 1) / bm) * ((a.columns + bn - 1) / bn);
+            const int64_t full = tiles / cus, rem = tiles % cus;
+            const double rounds = (double)full + (rem ? 0.7 + 0.3 * (double)rem / (double)cus : 0.0);
+            return rounds * (c * (double)a.width + e);
+        };
+        const double c6 = cost(256, 256, 0.0335, 13.6), c4 = cost(256, 128, 0.01435, 24.2),
+                     c5 = cost(128, 128, 0.0107, 8.1);
+        if (c6 <= c4 && c6 <= c5) return launch_ring16_cfg<256, 256, 4>(a, stream);
+        if (c4 <= c5) return launch_ring16_cfg<256, 128, 4>(a, stream);
+        return launch_ring16_cfg<128, 128, 4>(a, stream);
+    }
     const int64_t big_tiles = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
     if (big_tiles >= 512) return launch_mfma16_cfg<128, 128, 64, 2, 2, 4, 4>(a, stream);
     return launch_mfma16_cfg<64, 64, 64, 2, 2, 4, 4>(a, stream);
