@@ -1217,7 +1217,11 @@ __global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, i
     static_assert(kCpw <= 2 * FM * FN && kFrags <= 2 * FM * FN, "one read and copy per MFMA slot");
     static_assert((S - 1) * kOps < 64, "ops in flight within vmcnt");
     static_assert(WB != 4 || (KP == 2 && FM >= 2 && BN % 64 == 0), "int4 ring shape");
-    constexpr int FN4 = WB == 4 ? FN : 1;
+    // int4 and int8 codes: converted ahead, spread over the previous pair's
+    // MFMA slots (int8: 3-16 % faster than converting at the start of the
+    // pair on the four-wave and the eight-wave 256 x 256 rings, MI355X).
+    constexpr bool kPipe = WB == 4 || WB == 8;
+    constexpr int FN4 = kPipe ? FN : 1;
     static_assert(S * kStage + 4 * BN * 4 <= 160 * 1024 / OCC, "LDS");
     __shared__ __attribute__((aligned(1024))) uint8_t st0[kStage];
     __shared__ __attribute__((aligned(1024))) uint8_t st1[kStage];
@@ -1363,21 +1367,25 @@ __global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, i
         return (kXR * BM + (wn * WN + fr) / 2) * 64 + ((((fr & 1) * 2 + p) ^ ((fr >> 3) & 3)) << 4) + 8 * fh;
     };
     v4i xa0[FM][2], xb0[FN][kWH], xa1[FM][2], xb1[FN][kWH];
-    v8h bh0[FN4][2], bh1[FN4][2];  // int4: converted codes of a pair
+    v8h bh0[FN4][2], bh1[FN4][2];  // int4 / int8: converted codes of a pair
     uint16_t sc[FN4];              // int4: the K tile's bf16 scales (read with pair 0's codes)
-    // Fragment idx of a pair: A (i, j) for idx < 2 FM, else B idx - 2 FM
-    // (int8: column block idx - 2 FM; f16: block (idx - 2 FM) / 2, half (idx - 2 FM) % 2).
-    // int4 reads its B blocks first, idx < FN (with pair 0, the tile's
-    // scales), then A idx - FN; kt is the K tile in stage s.
+    // Fragment idx of a pair: f16 weights read A (i, j) for idx < 2 FM, then
+    // B block (idx - 2 FM) / 2, half (idx - 2 FM) % 2; int8 and int4 codes
+    // read their B blocks first, idx < FN (int4 with pair 0: the tile's
+    // scales too), then A idx - FN. kt is the K tile in stage s.
     auto read_frag = [&](int s, int p, int idx, v4i (&xa)[FM][2], v4i (&xb)[FN][kWH], int kt) {
-        if constexpr (WB == 4) {
+        if constexpr (kPipe) {
             if (idx < FN) {
-                const uint2 w2 = *reinterpret_cast<const uint2*>(stage(s) + offB4(p) + idx * 16 * 64);
-                xb[idx][0] = v4i{(int)w2.x, (int)w2.y, 0, 0};
-                if (p == 0) {
-                    const int g = (int)(kbase + kt) / gdiv;
-                    sc[idx] = *reinterpret_cast<const uint16_t*>(stage(s) + kScOff + (wn * WN + 32 * idx + fr) * 4 +
-                                                                 (g & 1) * 2);
+                if constexpr (WB == 8) {
+                    xb[idx][0] = *reinterpret_cast<const v4i*>(stage(s) + offB(p) + idx * 32 * 64);
+                } else {
+                    const uint2 w2 = *reinterpret_cast<const uint2*>(stage(s) + offB4(p) + idx * 16 * 64);
+                    xb[idx][0] = v4i{(int)w2.x, (int)w2.y, 0, 0};
+                    if (p == 0) {
+                        const int g = (int)(kbase + kt) / gdiv;
+                        sc[idx] = *reinterpret_cast<const uint16_t*>(stage(s) + kScOff +
+                                                                     (wn * WN + 32 * idx + fr) * 4 + (g & 1) * 2);
+                    }
                 }
             } else {
                 const int i = idx - FN;
@@ -1386,20 +1394,15 @@ __global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, i
         } else if (idx < 2 * FM) {
             xa[idx >> 1][idx & 1] =
                 *reinterpret_cast<const v4i*>(stage(s) + offA(p, idx & 1) + (idx >> 1) * 32 * 64);
-        } else if constexpr (WB == 8) {
-            xb[idx - 2 * FM][0] = *reinterpret_cast<const v4i*>(stage(s) + offB(p) + (idx - 2 * FM) * 32 * 64);
         } else {
             const int b = idx - 2 * FM;
             xb[b >> 1][b & 1] = *reinterpret_cast<const v4i*>(stage(s) + offB16(p, b & 1) + (b >> 1) * 32 * 64);
         }
     };
-    // One pair of MFMA steps on fragments xa/xb, with one read (and one copy)
-    // issued after each of the first MFMAs. The W codes of every column block
-    // are converted first; then the k 0..7 products of all FM x FN blocks run,
-    // then the k 8..15 ones, so no MFMA waits for the one just before it (two
-    // back-to-back MFMAs into one accumulator would serialise).
-    // int4: piece pc of a pair's conversion, codes 4 (pc % 4) .. +3 of block
-    // pc / 4 (i4x8_to_f16x8's steps, then times the scale), eight VALU ops.
+
+    // Piece pc of a pair's conversion: codes 4 (pc % 4) .. +3 of block pc / 4
+    // (int4: i4x8_to_f16x8's steps, then times the scale, eight VALU ops;
+    // int8: i8x4_to_f16x4, five).
     auto conv4 = [&](int pc, v4i (&xb)[FN][kWH], v8h (&bh)[FN4][2]) {
         if constexpr (WB == 4) {
             const int jn = pc >> 2, w = (pc >> 1) & 1, hc = pc & 1;
@@ -1414,12 +1417,20 @@ __global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, i
             bh[jn][w][4 * hc + 1] = h0[1];
             bh[jn][w][4 * hc + 2] = h1[0];
             bh[jn][w][4 * hc + 3] = h1[1];
+        } else if constexpr (WB == 8) {
+            const int jn = pc >> 2, q = pc & 3;
+            v2h h0, h1;
+            i8x4_to_f16x4((u32)xb[jn][0][q], h0, h1);
+            bh[jn][q >> 1][4 * (q & 1)] = h0[0];
+            bh[jn][q >> 1][4 * (q & 1) + 1] = h0[1];
+            bh[jn][q >> 1][4 * (q & 1) + 2] = h1[0];
+            bh[jn][q >> 1][4 * (q & 1) + 3] = h1[1];
         }
     };
     // After MFMA slot q: the conversion pieces that slot carries, spread
     // evenly from slot 3 on (block jn's codes are read at slot jn).
     auto conv_at = [&](int q, v4i (&xb)[FN][kWH], v8h (&bh)[FN4][2]) {
-        if constexpr (WB == 4) {
+        if constexpr (kPipe) {
             constexpr int ns = 2 * FM * FN, np = 4 * FN, c0 = 3;
 #pragma unroll
             for (int i = 0; i < np; ++i)
@@ -1427,22 +1438,14 @@ __global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, i
         }
     };
     v16f acc[FM][FN];
+    // One pair of MFMA steps on fragments xa and xb (f16 weights, fed to the
+    // MFMA straight from their fragment registers) or bq (int8 / int4 codes
+    // converted during the previous pair), with one read (and one copy, and
+    // conversion pieces) issued after each MFMA. The k 0..7 products of all
+    // FM x FN blocks run, then the k 8..15 ones, so no MFMA waits for the one
+    // just before it (two back-to-back MFMAs into one accumulator would
+    // serialise).
     auto pair_mfmas = [&](v4i (&xa)[FM][2], v4i (&xb)[FN][kWH], const v8h (&bq)[FN4][2], auto&& after) {
-        // f16 weights (WB = 16) feed the MFMA straight from their fragment
-        // registers; int8 weights are converted into bh first; int4 ones
-        // arrive converted in bq.
-        v8h bh[WB == 8 ? FN : 1][2];
-        if constexpr (WB == 8) {
-#pragma unroll
-            for (int jn = 0; jn < FN; ++jn) {
-                const u32 wd[4] = {(u32)xb[jn][0][0], (u32)xb[jn][0][1], (u32)xb[jn][0][2], (u32)xb[jn][0][3]};
-                v2h h[8];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) i8x4_to_f16x4(wd[q], h[2 * q], h[2 * q + 1]);
-                bh[jn][0] = v8h{h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
-                bh[jn][1] = v8h{h[4][0], h[4][1], h[5][0], h[5][1], h[6][0], h[6][1], h[7][0], h[7][1]};
-            }
-        }
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
 #pragma unroll
@@ -1451,9 +1454,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, i
                 for (int i = 0; i < FM; ++i) {
                     v8h av, bv;
                     __builtin_memcpy(&av, &xa[i][half], 16);
-                    if constexpr (WB == 8)
-                        bv = bh[jn][half];
-                    else if constexpr (WB == 4)
+                    if constexpr (kPipe)
                         bv = bq[jn][half];
                     else
                         __builtin_memcpy(&bv, &xb[jn][half * (kWH - 1)], 16);
@@ -1829,8 +1830,11 @@ W16Plan plan_w8a16(const W8A16Args& a, int cus, bool ws_limited) {
         const double rounds = (double)full + (rem ? 0.7 + 0.3 * (double)rem / (double)cus : 0.0);
         return Cand{(double)(bm * bn) * (c * (double)a.width + e) * rounds, id, tiles};
     };
-    Cand best = cost(17, 0.3566, 401.8, 256, 256);
-    for (const Cand& c : {cost(9, 0.4273, 399.1, 256, 192), cost(16, 0.4289, 201.6, 128, 256)})
+    // (The 256 x 256 and 256 x 192 fits are scaled by 0.94 and 0.90: spreading
+    // the code conversion over the MFMA slots made those rings 3-14 % and
+    // 6-16 % faster on eight of these shapes, the 128 x 256 one 0-3 % slower.)
+    Cand best = cost(17, 0.3352, 377.7, 256, 256);
+    for (const Cand& c : {cost(9, 0.3846, 359.2, 256, 192), cost(16, 0.4289, 201.6, 128, 256)})
         if (c.t < best.t) best = c;
     if (2 * best.tiles >= cus) return with_splits(best.id);
     // Fewer tiles than half the CUs: 64 x 128 tiles three workgroups per CU
