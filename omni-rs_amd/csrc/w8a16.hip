@@ -1765,8 +1765,9 @@ hipError_t launch_w8a16_skinny(const W8A16Args& a, hipStream_t stream) { return 
 // 1 = tiled 128 x 128, 2 = tiled 64 x 64, 4/5/6 = ring 256 x 128 / 128 x 128 /
 // 256 x 256 (2 x 2 waves), 7 = ring 256 x 256 (1 x 4 waves), 8 = ring
 // 64 x 128, 9 = ring 256 x 192, 10 = ring 128 x 128 two workgroups per CU,
-// 11 / 12 = ring 64 x 128 two / three per CU, 16 / 17 = ring 128 x 256 /
-// 256 x 256 with eight waves (rings: K % 64 == 0 only). OMNI_W8A16_SPLITS=<n>
+// 11 / 12 = ring 64 x 128 two / three per CU, 16 / 17 / 18 = ring 128 x 256 /
+// 256 x 256 (waves 64 x 128) / 256 x 256 (waves 128 x 64) with eight waves
+// (rings: K % 64 == 0 only). OMNI_W8A16_SPLITS=<n>
 // adds n-way split K to a pinned ring (or to the shape rule's choice) when
 // the call brings a workspace. Both are read on every call.
 int w8a16_tile_override() {
@@ -1789,7 +1790,7 @@ W16Plan plan_w8a16(const W8A16Args& a, int cus, bool ws_limited) {
     const int split_override = sv ? std::atoi(sv) : 0;
     const bool ring_ok = ring16_fits(a);
     const int ov = w8a16_tile_override();
-    if (ov == 1 || ov == 2 || (ov >= 4 && ov <= 12 && ring_ok) || ((ov == 16 || ov == 17) && ring_ok))
+    if (ov == 1 || ov == 2 || (ov >= 4 && ov <= 12 && ring_ok) || (ov >= 16 && ov <= 18 && ring_ok))
         return {ov, ov >= 4 && split_override > 1 ? split_override : 1};
     if (!ring_ok) {
         const int64_t big_tiles = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
@@ -1832,8 +1833,11 @@ W16Plan plan_w8a16(const W8A16Args& a, int cus, bool ws_limited) {
     };
     // (The 256 x 256 and 256 x 192 fits are scaled by 0.94 and 0.90: spreading
     // the code conversion over the MFMA slots made those rings 3-14 % and
-    // 6-16 % faster on eight of these shapes, the 128 x 256 one 0-3 % slower.)
-    Cand best = cost(17, 0.3352, 377.7, 256, 256);
+    // 6-16 % faster on eight of these shapes, the 128 x 256 one 0-3 % slower.
+    // The 256 x 256 candidate is then the eight-wave ring with two waves
+    // along M (each 128 x 64, half the conversions per MFMA of the 64 x 128
+    // one): 0.93-0.96 of that one's time on five shapes, so 0.95 of its fit.)
+    Cand best = cost(18, 0.3184, 358.8, 256, 256);
     for (const Cand& c : {cost(9, 0.3846, 359.2, 256, 192), cost(16, 0.4289, 201.6, 128, 256)})
         if (c.t < best.t) best = c;
     if (2 * best.tiles >= cus) return with_splits(best.id);
@@ -1878,6 +1882,7 @@ hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream) {
         case 11: return launch_ring16_cfg<64, 128, 8, 2, 3, 2, 2>(a, stream, sp);
         case 16: return launch_ring16_cfg<128, 256, 8, 2, 3, 2, 1, 8>(a, stream, sp);
         case 17: return launch_ring16_cfg<256, 256, 8, 4, 3, 2, 1, 8>(a, stream, sp);
+        case 18: return launch_ring16_cfg<256, 256, 8, 2, 3, 2, 1, 8>(a, stream, sp);
         default: return launch_ring16_cfg<64, 128, 8, 2, 3, 2, 3>(a, stream, sp);
     }
 }
@@ -1931,7 +1936,8 @@ hipError_t launch_w4a16_skinny(const W8A16Args& a, hipStream_t stream) {
 // OMNI_W4A16_TILE=<n> pins the W4A16 GEMM kernel (tuning and test aid):
 // 1 / 2 = tiled 128 x 128 / 64 x 64 (codes dequantized through registers),
 // rings 4 / 5 / 6 = 256 x 128 / 128 x 128 / 256 x 256, 10 = 128 x 128 at
-// two workgroups per CU, 16 / 17 = eight-wave 128 x 256 / 256 x 256
+// two workgroups per CU, 16 / 17 / 18 = eight-wave 128 x 256 / 256 x 256
+// (waves 64 x 128) / 256 x 256 (waves 128 x 64)
 // (rings: K % 64 == 0, group % 64 == 0 and K / group even). Read on every call.
 hipError_t launch_w4a16_mfma(const W8A16Args& a, hipStream_t stream) {
     if (a.rows == 0 || a.columns == 0) return hipSuccess;
@@ -1947,14 +1953,16 @@ hipError_t launch_w4a16_mfma(const W8A16Args& a, hipStream_t stream) {
         case 10: if (ring_ok) return launch_ring16_cfg<128, 128, 4, 2, 3, 2, 2>(a, stream); break;
         case 16: if (ring_ok) return launch_ring16_cfg<128, 256, 4, 2, 3, 2, 1, 8>(a, stream); break;
         case 17: if (ring_ok) return launch_ring16_cfg<256, 256, 4, 4, 3, 2, 1, 8>(a, stream); break;
+        case 18: if (ring_ok) return launch_ring16_cfg<256, 256, 4, 2, 3, 2, 1, 8>(a, stream); break;
         default: break;
     }
     if (ring_ok) {
-        // Rings 256 x 256 / 256 x 128 / 128 x 128, whichever a rounds cost
-        // model picks: tiles run in rounds of one per CU, a partial last round
-        // with fill f costs 0.7 + 0.3 f of a full one, and a full round costs
-        // c K + e us (MI355X fits over M = 256..4096, K = 3584..18944:
-        // 0.0335 K + 13.6, 0.01435 K + 24.2, 0.0107 K + 8.1).
+        // Rings 256 x 256 (eight waves, each 128 x 64) / 256 x 128 / 128 x 128,
+        // whichever a rounds cost model picks: tiles run in rounds of one per
+        // CU, a partial last round with fill f costs 0.7 + 0.3 f of a full
+        // one, and a full round costs c K + e us (MI355X fits over M =
+        // 256..4096, K = 3584..18944: 0.02488 K + 31.4, 0.01435 K + 24.2,
+        // 0.0107 K + 8.1).
         const int64_t cus = cu_count();
         auto cost = [&](int64_t bm, int64_t bn, double c, double e) {
             const int64_t tiles = ((a.rows + bm - 1) / bm) * ((a.columns + bn - 1) / bn);
@@ -1962,9 +1970,9 @@ hipError_t launch_w4a16_mfma(const W8A16Args& a, hipStream_t stream) {
             const double rounds = (double)full + (rem ? 0.7 + 0.3 * (double)rem / (double)cus : 0.0);
             return rounds * (c * (double)a.width + e);
         };
-        const double c6 = cost(256, 256, 0.0335, 13.6), c4 = cost(256, 128, 0.01435, 24.2),
+        const double c18 = cost(256, 256, 0.02488, 31.4), c4 = cost(256, 128, 0.01435, 24.2),
                      c5 = cost(128, 128, 0.0107, 8.1);
-        if (c6 <= c4 && c6 <= c5) return launch_ring16_cfg<256, 256, 4>(a, stream);
+        if (c18 <= c4 && c18 <= c5) return launch_ring16_cfg<256, 256, 4, 2, 3, 2, 1, 8>(a, stream);
         if (c4 <= c5) return launch_ring16_cfg<256, 128, 4>(a, stream);
         return launch_ring16_cfg<128, 128, 4>(a, stream);
     }
@@ -1992,7 +2000,8 @@ hipError_t launch_f16_skinny(const W8A16Args& a, hipStream_t stream) { return la
 // 1 = tiled 128 x 128, 2 = tiled 64 x 64, 4/5/6 = ring 256 x 128 / 128 x 128 /
 // 128 x 256, 7/8 = ring 256 x 256 / 256 x 128 on 32-element K tiles, 10 =
 // eight-wave ring 256 x 128, 12 / 13 = eight-wave ring 256 x 256 on 32- /
-// 64-element K tiles (rings: K % 64 == 0 only). Read on every call.
+// 64-element K tiles, 14 = the latter with waves 128 x 64 instead of 64 x 128
+// (rings: K % 64 == 0 only). Read on every call.
 hipError_t launch_f16_mfma(const W8A16Args& a, hipStream_t stream) {
     if (a.rows == 0 || a.columns == 0) return hipSuccess;
     const bool ring_ok = ring16_fits(a);
@@ -2008,6 +2017,7 @@ hipError_t launch_f16_mfma(const W8A16Args& a, hipStream_t stream) {
         case 10: if (ring_ok) return launch_ring16_cfg<256, 128, 16, 4, 3, 2, 1, 8>(a, stream); break;
         case 12: if (ring_ok) return launch_ring16_cfg<256, 256, 16, 4, 3, 1, 1, 8>(a, stream); break;
         case 13: if (ring_ok) return launch_ring16_cfg<256, 256, 16, 4, 2, 2, 1, 8>(a, stream); break;
+        case 14: if (ring_ok) return launch_ring16_cfg<256, 256, 16, 2, 2, 2, 1, 8>(a, stream); break;
         default: break;
     }
     const int64_t cus = cu_count();

@@ -149,12 +149,13 @@ def test_tensorops_shapes(oracle, rows, k, n):
     check(got_h[idx], oracle.f16_linear_f64(xs, host(w)), ("oracle rows", rows, k, n))
 
 
-@pytest.mark.parametrize("tile", ["1", "2", "4", "5", "6", "7", "8", "10", "12", "13"])
+@pytest.mark.parametrize("tile", ["1", "2", "4", "5", "6", "7", "8", "10", "12", "13", "14"])
 def test_every_gemm_kernel(oracle, monkeypatch, tile):
     # OMNI_F16_TILE pins one kernel: tiled 128 x 128 / 64 x 64, ring 256 x 128,
     # 128 x 128, 128 x 256, the 32-element-K-tile rings 256 x 256 and
     # 256 x 128, and the eight-wave rings 256 x 128 and 256 x 256 (32- and
-    # 64-element K tiles); ragged row counts and a grid smaller than the CUs.
+    # 64-element K tiles; waves 64 x 128 or 128 x 64); ragged row counts and a
+    # grid smaller than the CUs.
     monkeypatch.setenv("OMNI_F16_TILE", tile)
     for rows, k, n in ((300, 4096, 4160), (1000, 4160, 4096), (256, 12288, 12288)):
         x, w = rand_operands(rows, k, n, rows * 3 + int(tile))

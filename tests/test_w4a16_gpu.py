@@ -95,7 +95,7 @@ def test_guards():
         oi.w4a16_linear(x, w, s, group=100)   # group % 32 != 0: not handled
 
 
-@pytest.mark.parametrize("tile", ["1", "2", "4", "5", "6", "10", "16", "17"])
+@pytest.mark.parametrize("tile", ["1", "2", "4", "5", "6", "10", "16", "17", "18"])
 @pytest.mark.parametrize("rows,width,columns,group", [(300, 512, 200, 128), (1024, 1536, 1536, 128),
                                                       (257, 8960, 129, 64), (197, 4096, 640, 256),
                                                       (65, 64, 33, 64), (600, 4096, 700, 128),
@@ -103,8 +103,8 @@ def test_guards():
 def test_every_prefill_kernel(oracle, monkeypatch, tile, rows, width, columns, group):
     # OMNI_W4A16_TILE pins one prefill kernel: the tiled GEMMs (1, 2) and the
     # LDS-DMA rings on packed codes (4 = 256 x 128, 5 = 128 x 128, 6 = 256 x 256,
-    # 10 = 128 x 128 two per CU, 16 / 17 = 128 x 256 / 256 x 256 with eight
-    # waves; group 32 is not a ring case and takes the default); ragged
+    # 10 = 128 x 128 two per CU, 16 / 17 / 18 = 128 x 256 / 256 x 256 /
+    # 256 x 256 with eight waves; group 32 is not a ring case and takes the default); ragged
     # rows/columns, bias, against the f64 truth
     monkeypatch.setenv("OMNI_W4A16_TILE", tile)
     rng = np.random.default_rng(rows + width + columns + group + int(tile))
@@ -114,7 +114,7 @@ def test_every_prefill_kernel(oracle, monkeypatch, tile, rows, width, columns, g
     assert tolerance.rel_err(got, truth) <= tolerance.FP16_REL_TOL, (tile, rows, width, columns, group)
 
 
-@pytest.mark.parametrize("tile", ["4", "5", "16", "17"])
+@pytest.mark.parametrize("tile", ["4", "5", "16", "17", "18"])
 def test_ring_integer_inputs_are_exact(monkeypatch, tile):
     # integer x and unit scales through the rings: every product and f32
     # partial sum is an exact integer, rounded once to f16 as the int64 product is
