@@ -1938,11 +1938,14 @@ hipError_t launch_w4a16_skinny(const W8A16Args& a, hipStream_t stream) {
 // rings 4 / 5 / 6 = 256 x 128 / 128 x 128 / 256 x 256, 10 = 128 x 128 at
 // two workgroups per CU, 16 / 17 / 18 = eight-wave 128 x 256 / 256 x 256
 // (waves 64 x 128) / 256 x 256 (waves 128 x 64)
-// (rings: K % 64 == 0, group % 64 == 0 and K / group even). Read on every call.
+// (rings: K % 64 == 0, group % 64 == 0, K / group even, scales 4-byte
+// aligned). Read on every call.
 hipError_t launch_w4a16_mfma(const W8A16Args& a, hipStream_t stream) {
     if (a.rows == 0 || a.columns == 0) return hipSuccess;
-    // (the ring copies a column's scales as aligned bf16 pairs: an even count per row)
-    const bool ring_ok = ring16_fits(a) && a.group % 64 == 0 && (a.width / a.group) % 2 == 0;
+    // (the ring copies a column's scales as aligned bf16 pairs: an even count
+    // per row, from a 4-byte aligned scale array)
+    const bool ring_ok = ring16_fits(a) && a.group % 64 == 0 && (a.width / a.group) % 2 == 0 &&
+                         reinterpret_cast<uintptr_t>(a.gscale) % 4 == 0;
     const char* ov = std::getenv("OMNI_W4A16_TILE");
     switch (ov ? std::atoi(ov) : 0) {
         case 1: return launch_mfma16_cfg<128, 128, 64, 2, 2, 4, 4>(a, stream);

@@ -127,3 +127,21 @@ def test_ring_integer_inputs_are_exact(monkeypatch, tile):
         got = run(xr, wd.pack_int4(q), bits)
         want = (xr.astype(np.int64) @ q.astype(np.int64).T).astype(np.float16)
         assert np.array_equal(got, want), (tile, rows)
+
+
+@pytest.mark.parametrize("tile", ["0", "4", "18"])
+def test_scales_at_an_odd_bf16_offset(oracle, monkeypatch, tile):
+    # The rings copy scales as 4-byte pairs; a scale array starting 2 bytes
+    # past a 4-byte boundary (a contiguous view at an odd element) takes the
+    # register-staged kernel instead, with the same result bar
+    monkeypatch.setenv("OMNI_W4A16_TILE", tile)
+    rng = np.random.default_rng(int(tile) + 11)
+    x, packed, bits, b = wd.random_case(rng, 300, 1024, 200, 128, bias=True)
+    flat = np.concatenate([np.zeros(1, np.uint16), bits.reshape(-1)])
+    big = torch.from_numpy(flat.view(np.int16)).view(torch.bfloat16).cuda()
+    scale = big[1:].view(bits.shape)
+    assert scale.is_contiguous() and scale.data_ptr() % 4 == 2
+    got = oi.w4a16_linear(dev(x), dev(packed), scale, dev(b), group=128)
+    torch.cuda.synchronize()
+    truth = oracle.w4a16_f64(x, packed, bits, 128, b)
+    assert tolerance.rel_err(got.cpu().numpy().astype(np.float64), truth) <= tolerance.FP16_REL_TOL
