@@ -6,7 +6,7 @@
 //   code      = clamp(sign(x) * floor(|x / row_scale| + 0.5), -128, 127)
 //   sum       = sum of the row's codes
 //
-// Design: rows of up to 4096 elements take one wavefront each, rows of up to
+// Design: rows of up to 2048 elements take one wavefront each, rows of up to
 // 16384 one 256-lane workgroup each; either way the row is read once into
 // registers (16-element chunks, 128-bit loads), the peak is reduced across
 // the wave (and across the 4 waves through LDS), and the codes are written as
@@ -275,17 +275,17 @@ hipError_t launch_typed(const T* x, int64_t rows, int64_t width, int64_t ld, uin
         const int64_t align = in_bytes >= 16 ? 16 : in_bytes;
         return base % align == 0 && (ld * (int64_t)sizeof(T)) % align == 0 && cbase % vec == 0;
     };
-    // One wave per row up to 4 chunks per lane (4096 elements); wider rows
+    // One wave per row up to 2 chunks per lane (2048 elements); wider rows
     // (up to 16384) take a workgroup per row, 4 waves holding the row, which
-    // measured 15 % faster at 12288 f16 on MI355X than one wave per row.
-    if (width % 16 == 0 && width <= 4096 && aligned_for(16)) {
+    // measured faster on MI355X than one wave per row from 3072 f16 on (4096
+    // rows: 10.2 / 11.7 us against 10.6 / 14.1 at 3072 / 4096; 15 % at 12288)
+    // and slower at 1536 (8.5 against 7.4 us).
+    if (width % 16 == 0 && width <= 2048 && aligned_for(16)) {
         const int cpw = (int)((width / 16 + 63) / 64);
         dim3 grid((unsigned)((rows + 3) / 4)), block(256);
 #define OMNI_QWAVE(n) hipLaunchKernelGGL((quantize_rows_wave_kernel<T, n>), grid, block, 0, stream, x, rows, width, ld, codes, scale, sum)
         if (cpw <= 1) OMNI_QWAVE(1);
-        else if (cpw <= 2) OMNI_QWAVE(2);
-        else if (cpw <= 3) OMNI_QWAVE(3);
-        else OMNI_QWAVE(4);
+        else OMNI_QWAVE(2);
 #undef OMNI_QWAVE
         return hipGetLastError();
     }

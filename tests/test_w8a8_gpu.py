@@ -46,8 +46,8 @@ def run_gemm(x, w, scale, zero, lowering=oi.OMNI_LOWERING_AUTO, bias=None, out_d
 # -- quantisation ----------------------------------------------------------------
 
 
-@pytest.mark.parametrize("rows,width", [(1, 4), (3, 12), (17, 36), (5, 100), (64, 4096),
-                                        (7, 12288), (2, 4100)])
+@pytest.mark.parametrize("rows,width", [(1, 4), (3, 12), (17, 36), (5, 100), (9, 2048), (33, 2064),
+                                        (40, 3072), (64, 4096), (7, 12288), (2, 4100)])
 @pytest.mark.parametrize("dtype", [np.float32, np.float16])
 def test_quantize_rows_bit_exact(oracle, rows, width, dtype):
     rng = np.random.default_rng(rows * 1000 + width)
