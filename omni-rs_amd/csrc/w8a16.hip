@@ -1156,7 +1156,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void w8a16_mfma_kernel(W
 // v_mfma_f32_32x32x16_f16 takes codes and halves 0..7, the second 8..15: A and
 // B share one lane-to-k map, so every product pairs matching k and the 32 k
 // of the pair are summed once. Codes become f16 exactly in registers (v_perm
-// and one subtract, as in the GEMV). The schedule is the W8A8 ring's: one
+// and one subtract, as in the GEMV): a pair's codes are read before its x
+// halves and converted four at a time in the MFMA slots of the pair before
+// the one that uses them, so the conversion overlaps MFMAs instead of
+// preceding them. The schedule is the W8A8 ring's: one
 // fragment read and one copy behind each MFMA, one barrier per K tile between
 // the two pairs, the next tile's first copies issued before the epilogue. A
 // stage is refilled as soon as the barrier after its last fragment reads has
