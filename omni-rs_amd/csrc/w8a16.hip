@@ -1899,11 +1899,18 @@ hipError_t launch_w4a16_gemv(const W8A16Args& a, hipStream_t stream) {
     // workgroup (tuning aid); unset: the measured choice below.
     const char* ov = std::getenv("OMNI_W4A16_GEMV");
     int cfg = ov ? std::atoi(ov) : 0;
-    // Measured on MI355X: 4 rows per workgroup from 4 MB of codes (9.8 us
-    // at 4096 x 14336), two batches of 4 from 64 MB (53 us at the 128256-row
-    // vocabulary head, against 58 for one batch of 8), 2 rows below 4 MB.
+    // Measured on MI355X: 4 rows per workgroup from 4 MB of codes (7.6 us
+    // at 4096 x 14336), two batches of 4 from 64 MB (43 us at the 128256-row
+    // vocabulary head), 2 rows below 4 MB. With 2-4 activation rows, 8 rows
+    // per workgroup from 16 MB (4096 x 14336, 4 rows: 13.4 against 15.0 us;
+    // 14336 x 4096, 3 rows: 13.0 against 14.5; 4096 x 4096 stays on 4 rows,
+    // 6.3 against 7.9).
     const int64_t code_bytes = a.columns * a.width / 2;
-    if (cfg == 0) cfg = code_bytes >= (64 << 20) ? 42 : code_bytes >= (4 << 20) ? 41 : 21;
+    if (cfg == 0) {
+        if (code_bytes >= (64 << 20)) cfg = 42;
+        else if (a.rows >= 2 && code_bytes >= (16 << 20)) cfg = 81;
+        else cfg = code_bytes >= (4 << 20) ? 41 : 21;
+    }
     auto go = [&](auto rt, auto bt) {
         constexpr int R = decltype(rt)::value, B = decltype(bt)::value;
         const dim3 grid((unsigned)((a.columns + R * B - 1) / (R * B))), block((unsigned)T);
