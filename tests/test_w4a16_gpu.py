@@ -145,3 +145,19 @@ def test_scales_at_an_odd_bf16_offset(oracle, monkeypatch, tile):
     torch.cuda.synchronize()
     truth = oracle.w4a16_f64(x, packed, bits, 128, b)
     assert tolerance.rel_err(got.cpu().numpy().astype(np.float64), truth) <= tolerance.FP16_REL_TOL
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_default_routing_random_shapes(oracle, seed):
+    # The default kernel choice (GEMV, skinny, ring by the rounds model, or
+    # the register-staged fallback) on random shapes: rows 1..700, widths
+    # multiples of 64 with groups 64..256 (odd and even group counts)
+    rng = np.random.default_rng(1000 + seed)
+    rows = int(rng.choice([1, 3, 17, 64, 65, 200, 333, 700]))
+    group = int(rng.choice([64, 128, 256]))
+    width = group * int(rng.integers(1, 13))
+    columns = int(rng.integers(1, 900))
+    x, packed, bits, b = wd.random_case(rng, rows, width, columns, group, bias=bool(seed % 2))
+    got = run(x, packed, bits, b, group).astype(np.float64)
+    truth = oracle.w4a16_f64(x, packed, bits, group, b)
+    assert tolerance.rel_err(got, truth) <= tolerance.FP16_REL_TOL, (rows, width, columns, group)

@@ -303,3 +303,18 @@ def test_skinny_split_k_workspace_size():
     assert L.omni_w8a16_gemm_workspace_size(16, 8192, 4160) == 0                   # K % 256 != 0
     assert L.omni_w8a16_gemm_workspace_size(16, 8192, 8192) == 0                   # K > 4096
     assert L.omni_w8a16_gemm_workspace_size(17, 14336, 4096) == 0                  # skinny, not split
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_default_routing_random_shapes(oracle, seed):
+    # The default kernel choice (GEMV, skinny, split skinny, the rings by the
+    # rounds model with or without split K, or the tiled fallback) on random
+    # shapes: rows 1..900, widths multiples of 16 up to 9000
+    rng = np.random.default_rng(2000 + seed)
+    rows = int(rng.choice([1, 2, 4, 5, 16, 17, 64, 65, 300, 900]))
+    width = 16 * int(rng.integers(1, 560))
+    columns = int(rng.integers(1, 1200))
+    x, w, s, b = make(rng, rows, width, columns, bias=bool(seed % 2))
+    got = host(oi.w8a16_linear(dev(x), dev(w), dev(s), None if b is None else dev(b)))
+    ref = gpu_f64_reference(x, w, s, b)
+    assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL, (rows, width, columns)
