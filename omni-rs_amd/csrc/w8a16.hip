@@ -1843,6 +1843,15 @@ W16Plan plan_w8a16(const W8A16Args& a, int cus, bool ws_limited) {
     Cand best = cost(18, 0.3184, 358.8, 256, 256);
     for (const Cand& c : {cost(9, 0.3846, 359.2, 256, 192), cost(16, 0.4289, 201.6, 128, 256)})
         if (c.t < best.t) best = c;
+    // At most half a round of tiles and K >= 8192: split that ring's tiles
+    // 2-4 ways to about one unit per CU (1024 x 18944 -> 3584: 128 x 256
+    // tiles split two ways 155.9-158.7 us, against 194.6 on 64 x 128 tiles
+    // three per CU; 1024 x 14336 -> 4096: 126.8 against 153.7 unsplit).
+    if (a.width >= 8192 && 2 * best.tiles <= cus) {
+        const int64_t want = cus / best.tiles;
+        const int sp = split_override > 1 ? split_override : (int)(want < 2 ? 2 : want > 4 ? 4 : want);
+        if (!ws_limited || fit_splits(a, (int)(a.width / 64), sp) > 1) return {best.id, sp};
+    }
     if (2 * best.tiles >= cus) return with_splits(best.id);
     // Fewer tiles than half the CUs: 64 x 128 tiles three workgroups per CU
     // when they fit one round of those slots (config 5's 1024 x 1536 ->
