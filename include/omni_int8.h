@@ -237,6 +237,24 @@ int omni_w4a16_gemm(const uint16_t* x, const uint8_t* w_packed, const uint16_t* 
                     int64_t group, const uint16_t* bias, int64_t rows, int64_t columns,
                     int64_t width, uint16_t* out, void* stream);
 
+/* Bytes of workspace omni_w4a16_gemm_ws uses for this shape on the current
+ * device: split-K partial sums (f32 [splits][rows][columns]) for GEMM shapes
+ * (more than 64 rows) that split; 0 when the shape does not split. No
+ * counterpart in the reference: it serves omni_w4a16_gemm_ws. */
+size_t omni_w4a16_gemm_workspace_size(int64_t rows, int64_t columns, int64_t width, int64_t group);
+
+/* omni_w4a16_gemm with a caller-owned workspace (256-byte aligned, or NULL
+ * with workspace_bytes 0), which lets the GEMM split K across workgroups;
+ * with less than omni_w4a16_gemm_workspace_size bytes it splits less, with
+ * none it runs as omni_w4a16_gemm. Same contract otherwise (the split sums
+ * K in a different order: f32 rounding differs, not the operation). No
+ * counterpart in the reference: the extension of omni_w4a16_gemm that
+ * split K needs, as omni_w8a16_gemm_ws is for omni_w8a16_gemm. */
+int omni_w4a16_gemm_ws(const uint16_t* x, const uint8_t* w_packed, const uint16_t* scale_bf16,
+                       int64_t group, const uint16_t* bias, int64_t rows, int64_t columns,
+                       int64_t width, uint16_t* out, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
 /* fp16 decode GEMV, the Breeze TTS depth decoder's linear. Replaces
  * crates/breeze-tts/src/metal_depth.rs:84-123 (try_linear) and the kernel it
  * launches (gemv_kernel :13-35 via raw_gemv :36-83):

@@ -467,9 +467,24 @@ int omni_w8a16_gemm_ws(const uint16_t* x, const int8_t* w, const uint16_t* scale
     }
 }
 
+size_t omni_w4a16_gemm_workspace_size(int64_t rows, int64_t columns, int64_t width, int64_t group) {
+    if (rows <= 64 || columns <= 0 || width <= 0 || group <= 0 || width % 32 != 0 || group % 32 != 0 ||
+        width % group != 0)
+        return 0;
+    return (size_t)omni::w4a16_partial_elems(rows, columns, width, group) * sizeof(float);
+}
+
 int omni_w4a16_gemm(const uint16_t* x, const uint8_t* w_packed, const uint16_t* scale_bf16,
                     int64_t group, const uint16_t* bias, int64_t rows, int64_t columns,
                     int64_t width, uint16_t* out, void* stream) {
+    return omni_w4a16_gemm_ws(x, w_packed, scale_bf16, group, bias, rows, columns, width, out, nullptr, 0,
+                              stream);
+}
+
+int omni_w4a16_gemm_ws(const uint16_t* x, const uint8_t* w_packed, const uint16_t* scale_bf16,
+                       int64_t group, const uint16_t* bias, int64_t rows, int64_t columns,
+                       int64_t width, uint16_t* out, void* workspace, size_t workspace_bytes,
+                       void* stream) {
     if (rows < 0 || columns < 0 || width < 0 || group <= 0)
         return fail(OMNI_BAD_ARGUMENT, "w4a16_gemm: bad sizes");
     // 32 values (16 bytes) per GEMV lane, and a lane's values in one group.
@@ -480,6 +495,8 @@ int omni_w4a16_gemm(const uint16_t* x, const uint8_t* w_packed, const uint16_t* 
     if (!x || !w_packed || !scale_bf16 || !out) return fail(OMNI_BAD_ARGUMENT, "w4a16_gemm: null pointer");
     if (!aligned(x, 16) || !aligned(w_packed, 16))
         return fail(OMNI_BAD_ARGUMENT, "w4a16_gemm: x and w_packed must be 16-byte aligned");
+    if (workspace_bytes > 0 && (!workspace || !aligned(workspace, 256)))
+        return fail(OMNI_BAD_ARGUMENT, "w4a16_gemm: workspace must be 256-byte aligned");
     if (((rows + 63) / 64) * ((columns + 63) / 64) > 0x7fffffffLL)
         return fail(OMNI_BAD_ARGUMENT, "w4a16_gemm: problem too large");
     int st = check_current_device();
@@ -495,6 +512,8 @@ int omni_w4a16_gemm(const uint16_t* x, const uint8_t* w_packed, const uint16_t* 
     a.width = width;
     a.gscale = scale_bf16;
     a.group = group;
+    a.partial = static_cast<float*>(workspace);
+    a.partial_elems = (int64_t)(workspace_bytes / sizeof(float));
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (rows <= 4 && width <= 32768)
         return hip_status(omni::launch_w4a16_gemv(a, s), "w4a16 gemv launch");

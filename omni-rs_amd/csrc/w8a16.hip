@@ -1667,7 +1667,7 @@ __global__ __launch_bounds__(256) void w8a16_split_reduce_kernel(W8A16Args a, in
     _Float16 o[4];
     for (int e = 0; e < e_end; ++e) {
         if (e > 0 && ++c == a.columns) c = 0;
-        const float sc = (float)a.scale[c];
+        const float sc = a.scale ? (float)a.scale[c] : 1.0f;  // int4: scaled in the kernel
         const float bi = a.bias ? (float)a.bias[c] : 0.0f;
         o[e] = (_Float16)(v[e] * sc + bi);
     }
@@ -1714,7 +1714,7 @@ template <int BM, int BN, int WB = 8, int WMW = 2, int S = 3, int KP = 2, int OC
 hipError_t launch_ring16_cfg(const W8A16Args& a, hipStream_t stream, int splits = 1) {
     const int64_t tiles = ((a.rows + BM - 1) / BM) * ((a.columns + BN - 1) / BN);
     const int64_t slots = (int64_t)cu_count() * OCC;
-    if constexpr (WB == 8) {
+    if constexpr (WB == 8 || WB == 4) {
         // Split K when asked for and the partial sums fit (else fewer splits).
         if (splits > 1) splits = fit_splits(a, (int)(a.width / 64), splits);
         while (splits > 1 && tiles * splits > INT32_MAX) --splits;  // unit indices are int
@@ -1956,51 +1956,98 @@ hipError_t launch_w4a16_skinny(const W8A16Args& a, hipStream_t stream) {
 // 1 / 2 = tiled 128 x 128 / 64 x 64 (codes dequantized through registers),
 // rings 4 / 5 / 6 = 256 x 128 / 128 x 128 / 256 x 256, 10 = 128 x 128 at
 // two workgroups per CU, 16 / 17 / 18 = eight-wave 128 x 256 / 256 x 256
-// (waves 64 x 128) / 256 x 256 (waves 128 x 64)
-// (rings: K % 64 == 0, group % 64 == 0, K / group even, scales 4-byte
-// aligned). Read on every call.
+// (waves 64 x 128) / 256 x 256 (waves 128 x 64) (rings: K % 64 == 0, group
+// % 64 == 0, K / group even, scales 4-byte aligned); OMNI_W4A16_SPLITS=<n>
+// adds n-way split K to a pinned ring when the call brings a workspace.
+// Both are read on every call.
+struct W4Plan {
+    int cfg;     // tile id as above
+    int splits;  // K splits (> 1 needs a workspace)
+};
+
+// (the ring copies a column's scales as aligned bf16 pairs: an even count
+// per row, from a 4-byte aligned scale array)
+bool w4_ring_ok(const W8A16Args& a) {
+    return ring16_fits(a) && a.group % 64 == 0 && (a.width / a.group) % 2 == 0 &&
+           reinterpret_cast<uintptr_t>(a.gscale) % 4 == 0;
+}
+
+W4Plan plan_w4a16(const W8A16Args& a, int cus, bool ws_limited) {
+    const char* sv = std::getenv("OMNI_W4A16_SPLITS");
+    const int split_override = sv ? std::atoi(sv) : 0;
+    const char* ov = std::getenv("OMNI_W4A16_TILE");
+    const int t = ov ? std::atoi(ov) : 0;
+    const bool ring_ok = w4_ring_ok(a);
+    if (t == 1 || t == 2) return {t, 1};
+    if (ring_ok && (t == 4 || t == 5 || t == 6 || t == 10 || (t >= 16 && t <= 18)))
+        return {t, split_override > 1 ? split_override : 1};
+    if (!ring_ok) {
+        const int64_t big_tiles = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
+        return {big_tiles >= 512 ? 1 : 2, 1};
+    }
+    // Rings 256 x 256 (eight waves, each 128 x 64) / 256 x 128 / 128 x 128,
+    // each unsplit or with K split 2-4 ways, whichever a rounds cost model
+    // picks: units (tiles, or tiles x splits) run in rounds of one per CU, a
+    // partial last round with fill f costs 0.7 + 0.3 f of a full one, a full
+    // round costs c K' + e us for K' = K / splits (MI355X fits over M =
+    // 256..4096, K = 3584..18944: 0.02488 K' + 31.4, 0.01435 K' + 24.2,
+    // 0.0107 K' + 8.1), and a split adds its reduction, 1 us + (4 splits + 2)
+    // bytes per output at 3.5 TB/s; K < 4096 is not split. On seven long-K
+    // shapes it picks within 5 % of the fastest of eleven ring/split choices
+    // (1024 x 14336 -> 4096: 137-139 us split, against 166 unsplit;
+    // 1024 x 8960 -> 1536: 55 against 85).
+    const int ktiles = (int)(a.width / 64);
+    double best_t = 0.0;
+    W4Plan best{5, 1};
+    auto consider = [&](int id, int64_t bm, int64_t bn, double c, double e) {
+        const int64_t tiles = ((a.rows + bm - 1) / bm) * ((a.columns + bn - 1) / bn);
+        for (int sp = 1; sp <= 4; ++sp) {
+            if (sp > 1 && (a.width < 4096 || (ws_limited && fit_splits(a, ktiles, sp) != sp))) break;
+            const int64_t units = tiles * sp;
+            const int64_t full = units / cus, rem = units % cus;
+            const double rounds = (double)full + (rem ? 0.7 + 0.3 * (double)rem / (double)cus : 0.0);
+            double t = rounds * (c * (double)a.width / sp + e);
+            if (sp > 1) t += 1.0 + (4.0 * sp + 2.0) * (double)a.rows * (double)a.columns / 3.5e6;
+            if (best_t == 0.0 || t < best_t) {
+                best_t = t;
+                best = {id, sp};
+            }
+        }
+    };
+    consider(18, 256, 256, 0.02488, 31.4);
+    consider(4, 256, 128, 0.01435, 24.2);
+    consider(5, 128, 128, 0.0107, 8.1);
+    if (split_override > 1 && (!ws_limited || fit_splits(a, ktiles, split_override) > 1))
+        return {best.cfg, split_override};
+    return best;
+}
+
+int64_t w4a16_partial_elems(int64_t rows, int64_t columns, int64_t width, int64_t group) {
+    if (rows <= 0 || columns <= 0 || group <= 0) return 0;
+    W8A16Args a{};
+    a.rows = rows;
+    a.columns = columns;
+    a.width = width;
+    a.group = group;
+    const W4Plan p = plan_w4a16(a, cu_count(), false);
+    return p.cfg >= 4 && p.splits > 1 ? (int64_t)p.splits * rows * columns : 0;
+}
+
 hipError_t launch_w4a16_mfma(const W8A16Args& a, hipStream_t stream) {
     if (a.rows == 0 || a.columns == 0) return hipSuccess;
-    // (the ring copies a column's scales as aligned bf16 pairs: an even count
-    // per row, from a 4-byte aligned scale array)
-    const bool ring_ok = ring16_fits(a) && a.group % 64 == 0 && (a.width / a.group) % 2 == 0 &&
-                         reinterpret_cast<uintptr_t>(a.gscale) % 4 == 0;
-    const char* ov = std::getenv("OMNI_W4A16_TILE");
-    switch (ov ? std::atoi(ov) : 0) {
+    const W4Plan p = plan_w4a16(a, cu_count(), true);
+    const int sp = p.splits;
+    switch (p.cfg) {
         case 1: return launch_mfma16_cfg<128, 128, 64, 2, 2, 4, 4>(a, stream);
         case 2: return launch_mfma16_cfg<64, 64, 64, 2, 2, 4, 4>(a, stream);
-        case 4: if (ring_ok) return launch_ring16_cfg<256, 128, 4>(a, stream); break;
-        case 5: if (ring_ok) return launch_ring16_cfg<128, 128, 4>(a, stream); break;
-        case 6: if (ring_ok) return launch_ring16_cfg<256, 256, 4>(a, stream); break;
-        case 10: if (ring_ok) return launch_ring16_cfg<128, 128, 4, 2, 3, 2, 2>(a, stream); break;
-        case 16: if (ring_ok) return launch_ring16_cfg<128, 256, 4, 2, 3, 2, 1, 8>(a, stream); break;
-        case 17: if (ring_ok) return launch_ring16_cfg<256, 256, 4, 4, 3, 2, 1, 8>(a, stream); break;
-        case 18: if (ring_ok) return launch_ring16_cfg<256, 256, 4, 2, 3, 2, 1, 8>(a, stream); break;
-        default: break;
+        case 4: return launch_ring16_cfg<256, 128, 4>(a, stream, sp);
+        case 5: return launch_ring16_cfg<128, 128, 4>(a, stream, sp);
+        case 6: return launch_ring16_cfg<256, 256, 4>(a, stream, sp);
+        case 10: return launch_ring16_cfg<128, 128, 4, 2, 3, 2, 2>(a, stream, sp);
+        case 16: return launch_ring16_cfg<128, 256, 4, 2, 3, 2, 1, 8>(a, stream, sp);
+        case 17: return launch_ring16_cfg<256, 256, 4, 4, 3, 2, 1, 8>(a, stream, sp);
+        default: return launch_ring16_cfg<256, 256, 4, 2, 3, 2, 1, 8>(a, stream, sp);
     }
-    if (ring_ok) {
-        // Rings 256 x 256 (eight waves, each 128 x 64) / 256 x 128 / 128 x 128,
-        // whichever a rounds cost model picks: tiles run in rounds of one per
-        // CU, a partial last round with fill f costs 0.7 + 0.3 f of a full
-        // one, and a full round costs c K + e us (MI355X fits over M =
-        // 256..4096, K = 3584..18944: 0.02488 K + 31.4, 0.01435 K + 24.2,
-        // 0.0107 K + 8.1).
-        const int64_t cus = cu_count();
-        auto cost = [&](int64_t bm, int64_t bn, double c, double e) {
-            const int64_t tiles = ((a.rows + bm - 1) / bm) * ((a.columns + bn - 1) / bn);
-            const int64_t full = tiles / cus, rem = tiles % cus;
-            const double rounds = (double)full + (rem ? 0.7 + 0.3 * (double)rem / (double)cus : 0.0);
-            return rounds * (c * (double)a.width + e);
-        };
-        const double c18 = cost(256, 256, 0.02488, 31.4), c4 = cost(256, 128, 0.01435, 24.2),
-                     c5 = cost(128, 128, 0.0107, 8.1);
-        if (c18 <= c4 && c18 <= c5) return launch_ring16_cfg<256, 256, 4, 2, 3, 2, 1, 8>(a, stream);
-        if (c4 <= c5) return launch_ring16_cfg<256, 128, 4>(a, stream);
-        return launch_ring16_cfg<128, 128, 4>(a, stream);
-    }
-    const int64_t big_tiles = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
-    if (big_tiles >= 512) return launch_mfma16_cfg<128, 128, 64, 2, 2, 4, 4>(a, stream);
-    return launch_mfma16_cfg<64, 64, 64, 2, 2, 4, 4>(a, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -253,9 +253,12 @@ def w4a16_linear(x: torch.Tensor, w_packed: torch.Tensor, scale: torch.Tensor,
     scale_c = scale.contiguous()
     bias_c = None if bias is None else bias.reshape(-1).contiguous()
     out = torch.empty((x2.shape[0], columns), dtype=torch.float16, device=device)
-    st = _lib.check(_lib.lib().omni_w4a16_gemm(
+    L = _lib.lib()
+    ws_bytes = L.omni_w4a16_gemm_workspace_size(x2.shape[0], columns, width, group)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes else None
+    st = _lib.check(L.omni_w4a16_gemm_ws(
         _ptr(x2), _ptr(w_c), _ptr(scale_c), group, _ptr(bias_c), x2.shape[0], columns, width,
-        _ptr(out), _stream(device)))
+        _ptr(out), _ptr(workspace), ws_bytes, _stream(device)))
     if st == OMNI_NOT_HANDLED:
         raise ValueError(_lib.last_error())
     return out.reshape(*lead, columns)

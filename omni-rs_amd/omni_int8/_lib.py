@@ -47,6 +47,8 @@ SIGNATURES = {
     "omni_w8a16_gemm_workspace_size": (ctypes.c_size_t, [_I64, _I64, _I64]),
     "omni_w8a16_gemm_ws": (_INT, [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, ctypes.c_size_t, _P]),
     "omni_w4a16_gemm": (_INT, [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _P]),
+    "omni_w4a16_gemm_workspace_size": (ctypes.c_size_t, [_I64, _I64, _I64, _I64]),
+    "omni_w4a16_gemm_ws": (_INT, [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _P, ctypes.c_size_t, _P]),
     "omni_f16_gemv": (_INT, [_P, _P, _I64, _I64, _I64, _P, _P]),
     "omni_f16_gemm": (_INT, [_P, _P, _I64, _I64, _I64, _P, _P]),
     "omni_convrot_quantize_rows": (_INT, [_P, _INT, _I64, _I64, _I64, _I64, _P, _P, _P, _P]),

@@ -161,3 +161,83 @@ def test_default_routing_random_shapes(oracle, seed):
     got = run(x, packed, bits, b, group).astype(np.float64)
     truth = oracle.w4a16_f64(x, packed, bits, group, b)
     assert tolerance.rel_err(got, truth) <= tolerance.FP16_REL_TOL, (rows, width, columns, group)
+
+
+_SPLIT_CASES = {}
+
+
+@pytest.mark.parametrize("tile", ["4", "5", "6", "10", "16", "17", "18"])
+@pytest.mark.parametrize("splits", ["2", "3", "4"])
+@pytest.mark.parametrize("rows,width,columns,group,bias", [(520, 4096, 300, 128, False),
+                                                           (300, 2048, 202, 64, True),
+                                                           (130, 768, 515, 256, True),
+                                                           (65, 128, 33, 64, False)])
+def test_split_k_every_ring(oracle, monkeypatch, tile, splits, rows, width, columns, group, bias):
+    # OMNI_W4A16_SPLITS forces split K on a pinned int4 ring: units of
+    # (tile, K range), f32 partial sums of the scaled codes, an in-order
+    # reduction adding bias. K tile counts 64, 32, 12 and 2 (uneven splits,
+    # fewer than asked when a split would be empty), ragged rows and columns,
+    # columns % 4 != 0 (the reduction's scalar path); deterministic. One
+    # case per shape, its f64 truth computed once.
+    monkeypatch.setenv("OMNI_W4A16_TILE", tile)
+    monkeypatch.setenv("OMNI_W4A16_SPLITS", splits)
+    key = (rows, width, columns, group, bias)
+    if key not in _SPLIT_CASES:
+        rng = np.random.default_rng(rows + width + columns)
+        x, packed, bits, b = wd.random_case(rng, rows, width, columns, group, bias=bias)
+        _SPLIT_CASES[key] = (x, packed, bits, b, oracle.w4a16_f64(x, packed, bits, group, b))
+    x, packed, bits, b, truth = _SPLIT_CASES[key]
+    scale = torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).cuda()
+    xd, pd, bd = dev(x), dev(packed), None if b is None else dev(b)
+    got = oi.w4a16_linear(xd, pd, scale, bd, group=group)
+    again = oi.w4a16_linear(xd, pd, scale, bd, group=group)
+    assert tolerance.rel_err(got.cpu().numpy().astype(np.float64), truth) <= tolerance.FP16_REL_TOL, \
+        (tile, splits, rows, width, columns)
+    assert torch.equal(got, again), "split K must be deterministic"
+
+
+def test_split_k_workspace_contract(oracle, monkeypatch):
+    # omni_w4a16_gemm_workspace_size reports splits * rows * columns floats
+    # for a split shape and 0 otherwise; omni_w4a16_gemm_ws splits less with
+    # a smaller workspace, not at all with none, and every result is within
+    # the bar.
+    from omni_int8 import _lib
+    L = _lib.lib()
+    monkeypatch.setenv("OMNI_W4A16_TILE", "4")
+    monkeypatch.setenv("OMNI_W4A16_SPLITS", "4")
+    rows, width, columns, group = 300, 4096, 260, 128
+    assert L.omni_w4a16_gemm_workspace_size(rows, columns, width, group) == 4 * rows * columns * 4
+    assert L.omni_w4a16_gemm_workspace_size(64, columns, width, group) == 0  # skinny route
+    assert L.omni_w4a16_gemm_workspace_size(4, columns, width, group) == 0  # GEMV
+    assert L.omni_w4a16_gemm_workspace_size(rows, columns, width, 96) == 0  # width % group != 0
+    monkeypatch.delenv("OMNI_W4A16_TILE")
+    monkeypatch.delenv("OMNI_W4A16_SPLITS")
+    # the launcher's own choice: MiniCPM-V's down projection at M = 1024
+    # splits, its K = 3584 linears do not
+    assert L.omni_w4a16_gemm_workspace_size(1024, 3584, 18944, 128) >= 2 * 1024 * 3584 * 4
+    assert L.omni_w4a16_gemm_workspace_size(1024, 18944, 3584, 128) == 0
+    monkeypatch.setenv("OMNI_W4A16_TILE", "4")
+    monkeypatch.setenv("OMNI_W4A16_SPLITS", "4")
+    rng = np.random.default_rng(79)
+    x, packed, bits, b = wd.random_case(rng, rows, width, columns, group, bias=True)
+    scale = torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).cuda()
+    xd, pd, bd = dev(x), dev(packed), dev(b)
+    truth = oracle.w4a16_f64(x, packed, bits, group, b)
+    stream = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for floats in (4 * rows * columns, 2 * rows * columns + 5, 0):
+        ws = torch.empty(max(floats, 1) * 4, dtype=torch.uint8, device="cuda")
+        out = torch.empty((rows, columns), dtype=torch.float16, device="cuda")
+        st = L.omni_w4a16_gemm_ws(xd.data_ptr(), pd.data_ptr(), scale.data_ptr(), group, bd.data_ptr(), rows,
+                                  columns, width, out.data_ptr(), ws.data_ptr() if floats else None, floats * 4,
+                                  stream)
+        assert st == 0, _lib.last_error()
+        assert tolerance.rel_err(out.cpu().numpy().astype(np.float64), truth) <= tolerance.FP16_REL_TOL, floats
+        outs.append(out)
+    monkeypatch.setenv("OMNI_W4A16_SPLITS", "1")
+    plain = oi.w4a16_linear(xd, pd, scale, bd, group=group)
+    assert torch.equal(outs[2], plain), "no workspace runs unsplit"
+    bad = torch.empty(1024, dtype=torch.uint8, device="cuda")
+    st = L.omni_w4a16_gemm_ws(xd.data_ptr(), pd.data_ptr(), scale.data_ptr(), group, bd.data_ptr(), rows, columns,
+                              width, outs[0].data_ptr(), bad.data_ptr() + 4, 512, stream)
+    assert st == _lib.OMNI_BAD_ARGUMENT
