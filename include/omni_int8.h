@@ -200,7 +200,8 @@ int omni_convrot_linear(const void* x, int x_dtype, int64_t rows, int64_t width,
  *   out[m][n] = f16(scale[n] * sum_k x[m][k] * w[n][k] + bias[n])
  * x f16 [rows][width], w int8 [columns][width], scale f16 [columns],
  * bias f16 [columns] or NULL, out f16 [rows][columns]. width % 16 == 0.
- * rows <= 4 with width <= 16384 runs the HBM-bound GEMV; other shapes run the
+ * rows <= 4 with width <= 16384 runs the HBM-bound GEMV, up to 16 rows (up
+ * to 64 on smaller matrices) the skinny MFMA kernel, more rows the
  * fp16-MFMA GEMM. */
 int omni_w8a16_gemm(const uint16_t* x, const int8_t* w, const uint16_t* scale,
                     const uint16_t* bias, int64_t rows, int64_t columns, int64_t width,
@@ -232,7 +233,8 @@ int omni_w8a16_gemm_ws(const uint16_t* x, const int8_t* w, const uint16_t* scale
  * x f16 [rows][width], bias f16 [columns] or NULL, out f16 [rows][columns].
  * width % group == 0 and group % 32 == 0, else OMNI_NOT_HANDLED; x and
  * w_packed 16-byte aligned. rows <= 4 (width <= 32768) runs the HBM-bound
- * GEMV, rows <= 64 the skinny MFMA kernel, more rows the fp16-MFMA GEMM. */
+ * GEMV, up to 16 rows (up to 64 on smaller matrices) the skinny MFMA kernel,
+ * more rows the fp16-MFMA GEMM. */
 int omni_w4a16_gemm(const uint16_t* x, const uint8_t* w_packed, const uint16_t* scale_bf16,
                     int64_t group, const uint16_t* bias, int64_t rows, int64_t columns,
                     int64_t width, uint16_t* out, void* stream);

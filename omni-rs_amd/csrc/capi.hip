@@ -75,21 +75,48 @@ bool force_scalar() {
 
 bool aligned(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
 
-// OMNI_W8A16_ROUTE=2 sends 5..64-row W8A16 calls to the tiled MFMA GEMM
-// instead of the skinny kernel (test aid; read on every call).
+// OMNI_W8A16_ROUTE=1 keeps 5..64-row W8A16 and W4A16 calls on the skinny
+// kernel, =2 sends them to the tiled MFMA GEMM (test aids; read on every
+// call); unset, the measured rule below.
 int w8a16_route() {
     const char* v = std::getenv("OMNI_W8A16_ROUTE");
     return v ? std::atoi(v) : 0;
 }
 
+// 17..64 rows: the skinny kernel streams the weights once per 16 rows, the
+// GEMM once per 64 to 256, so the GEMM wins on big matrices (MI355X, W8A16
+// 4096 -> 14336: 24.5 against 37.7 us at 24 rows, 27.4 against 70.5 at 64;
+// 4096 -> 4096 stays skinny to 48 rows: 15.5 against 16.8). W4A16 over a
+// long K (14336 -> 4096) stays skinny to 48 rows (40.3 against 43.4 at 32).
+bool midrows_take_gemm(int64_t rows, int64_t columns, int64_t width, bool int4) {
+    const double elems = (double)columns * (double)width;
+    if (rows > 48 && elems >= 16e6) return true;
+    if (int4 && columns < 2 * width) return false;
+    return elems >= 32e6;
+}
+
 // The W8A16 route: 0 GEMV, 1 skinny MFMA, 2 the GEMM.
-int w8a16_kind(int64_t rows, int64_t width) {
+int w8a16_kind(int64_t rows, int64_t columns, int64_t width) {
     // The GEMV spreads a row over one workgroup of at most 1024 lanes, one
     // 16-element chunk per lane: width <= 16384.
     if (rows <= 4 && width <= 16384) return 0;
-    // 5..64 rows: the weights are streamed once by a GEMV-shaped MFMA kernel.
-    if (rows <= 64 && w8a16_route() != 2) return 1;
-    return 2;
+    if (rows > 64) return 2;
+    // 5..64 rows: the weights are streamed once by a GEMV-shaped MFMA kernel
+    // up to 16 rows, and on small matrices beyond.
+    const int r = w8a16_route();
+    if (r == 1) return 1;
+    if (r == 2) return 2;
+    return rows > 16 && midrows_take_gemm(rows, columns, width, false) ? 2 : 1;
+}
+
+// The same for W4A16 (its GEMV takes width <= 32768).
+int w4a16_kind(int64_t rows, int64_t columns, int64_t width) {
+    if (rows <= 4 && width <= 32768) return 0;
+    if (rows > 64) return 2;
+    const int r = w8a16_route();
+    if (r == 1) return 1;
+    if (r == 2) return 2;
+    return rows > 16 && midrows_take_gemm(rows, columns, width, true) ? 2 : 1;
 }
 
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
@@ -419,7 +446,7 @@ int omni_convrot_linear(const void* x, int x_dtype, int64_t rows, int64_t width,
 
 size_t omni_w8a16_gemm_workspace_size(int64_t rows, int64_t columns, int64_t width) {
     if (rows <= 0 || columns <= 0 || width <= 0 || width % 16 != 0) return 0;
-    switch (w8a16_kind(rows, width)) {
+    switch (w8a16_kind(rows, columns, width)) {
         case 1: return (size_t)omni::w8a16_skinny_partial_elems(rows, columns, width) * sizeof(float);
         case 2: return (size_t)omni::w8a16_partial_elems(rows, columns, width) * sizeof(float);
         default: return 0;
@@ -460,7 +487,7 @@ int omni_w8a16_gemm_ws(const uint16_t* x, const int8_t* w, const uint16_t* scale
     a.partial = static_cast<float*>(workspace);
     a.partial_elems = (int64_t)(workspace_bytes / sizeof(float));
     hipStream_t s = static_cast<hipStream_t>(stream);
-    switch (w8a16_kind(rows, width)) {
+    switch (w8a16_kind(rows, columns, width)) {
         case 0: return hip_status(omni::launch_w8a16_gemv(a, s), "w8a16 gemv launch");
         case 1: return hip_status(omni::launch_w8a16_skinny(a, s), "w8a16 skinny launch");
         default: return hip_status(omni::launch_w8a16_mfma(a, s), "w8a16 mfma launch");
@@ -468,8 +495,8 @@ int omni_w8a16_gemm_ws(const uint16_t* x, const int8_t* w, const uint16_t* scale
 }
 
 size_t omni_w4a16_gemm_workspace_size(int64_t rows, int64_t columns, int64_t width, int64_t group) {
-    if (rows <= 64 || columns <= 0 || width <= 0 || group <= 0 || width % 32 != 0 || group % 32 != 0 ||
-        width % group != 0)
+    if (rows <= 0 || columns <= 0 || width <= 0 || group <= 0 || width % 32 != 0 || group % 32 != 0 ||
+        width % group != 0 || w4a16_kind(rows, columns, width) != 2)
         return 0;
     return (size_t)omni::w4a16_partial_elems(rows, columns, width, group) * sizeof(float);
 }
@@ -515,10 +542,11 @@ int omni_w4a16_gemm_ws(const uint16_t* x, const uint8_t* w_packed, const uint16_
     a.partial = static_cast<float*>(workspace);
     a.partial_elems = (int64_t)(workspace_bytes / sizeof(float));
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (rows <= 4 && width <= 32768)
-        return hip_status(omni::launch_w4a16_gemv(a, s), "w4a16 gemv launch");
-    if (rows <= 64) return hip_status(omni::launch_w4a16_skinny(a, s), "w4a16 skinny launch");
-    return hip_status(omni::launch_w4a16_mfma(a, s), "w4a16 mfma launch");
+    switch (w4a16_kind(rows, columns, width)) {
+        case 0: return hip_status(omni::launch_w4a16_gemv(a, s), "w4a16 gemv launch");
+        case 1: return hip_status(omni::launch_w4a16_skinny(a, s), "w4a16 skinny launch");
+        default: return hip_status(omni::launch_w4a16_mfma(a, s), "w4a16 mfma launch");
+    }
 }
 
 int omni_f16_gemv(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t columns,

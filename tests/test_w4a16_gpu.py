@@ -241,3 +241,17 @@ def test_split_k_workspace_contract(oracle, monkeypatch):
     st = L.omni_w4a16_gemm_ws(xd.data_ptr(), pd.data_ptr(), scale.data_ptr(), group, bd.data_ptr(), rows, columns,
                               width, outs[0].data_ptr(), bad.data_ptr() + 4, 512, stream)
     assert st == _lib.OMNI_BAD_ARGUMENT
+
+
+@pytest.mark.parametrize("route", ["0", "1", "2"])
+@pytest.mark.parametrize("rows,width,columns,group", [(24, 4096, 8200, 128), (40, 2048, 16400, 64),
+                                                      (40, 8192, 4100, 128), (17, 512, 300, 128)])
+def test_mid_rows_on_every_route(oracle, monkeypatch, route, rows, width, columns, group):
+    # 17..64 activation rows: the default choice (the first two shapes take
+    # the GEMM, the last two the skinny kernel), and each route forced
+    monkeypatch.setenv("OMNI_W8A16_ROUTE", route)
+    rng = np.random.default_rng(rows + width + columns + group)
+    x, packed, bits, b = wd.random_case(rng, rows, width, columns, group, bias=True)
+    got = run(x, packed, bits, b, group).astype(np.float64)
+    truth = oracle.w4a16_f64(x, packed, bits, group, b)
+    assert tolerance.rel_err(got, truth) <= tolerance.FP16_REL_TOL, (route, rows, width, columns)

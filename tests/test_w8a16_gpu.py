@@ -128,14 +128,15 @@ def test_mfma_gemm_shapes(oracle, rows, width, columns):
     assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL
 
 
-@pytest.mark.parametrize("route", ["0", "2"])
+@pytest.mark.parametrize("route", ["0", "1", "2"])
 @pytest.mark.parametrize("rows,width,columns", [(5, 64, 33), (16, 4096, 4096), (13, 4112, 77),
                                                 (33, 1552, 200), (48, 16384, 17), (64, 8960, 1536),
-                                                (7, 16, 3)])
+                                                (7, 16, 3), (40, 4096, 8200), (60, 2048, 8300)])
 def test_skinny_rows_on_both_routes(oracle, monkeypatch, route, rows, width, columns):
-    # 5..64 activation rows: the skinny MFMA kernel (route 0) and the tiled
-    # MFMA GEMM (OMNI_W8A16_ROUTE=2) against the f64 ground truth, with K
-    # tails that are not a multiple of 64 and ragged column counts.
+    # 5..64 activation rows: the default choice (route 0), the skinny MFMA
+    # kernel (OMNI_W8A16_ROUTE=1) and the tiled MFMA GEMM (=2) against the
+    # f64 ground truth, with K tails that are not a multiple of 64 and
+    # ragged column counts; the last two shapes take the GEMM by default.
     monkeypatch.setenv("OMNI_W8A16_ROUTE", route)
     rng = np.random.default_rng(rows * 3 + width + columns)
     x, w, s, b = make(rng, rows, width, columns, bias=columns % 2 == 1)
@@ -302,7 +303,10 @@ def test_skinny_split_k_workspace_size():
     assert L.omni_w8a16_gemm_workspace_size(16, 8192, 1024) == 0                   # K fits one unit
     assert L.omni_w8a16_gemm_workspace_size(16, 8192, 4160) == 0                   # K % 256 != 0
     assert L.omni_w8a16_gemm_workspace_size(16, 8192, 8192) == 0                   # K > 4096
-    assert L.omni_w8a16_gemm_workspace_size(17, 14336, 4096) == 0                  # skinny, not split
+    assert L.omni_w8a16_gemm_workspace_size(17, 4096, 4096) == 0                   # skinny, not split
+    # 17 rows of a 58.7 M-weight matrix take the GEMM, split K (64 x 128 tiles)
+    assert L.omni_w8a16_gemm_workspace_size(17, 14336, 4096) % (17 * 14336 * 4) == 0
+    assert L.omni_w8a16_gemm_workspace_size(17, 14336, 4096) >= 2 * 17 * 14336 * 4
 
 
 @pytest.mark.parametrize("seed", range(12))
