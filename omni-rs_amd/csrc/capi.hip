@@ -496,9 +496,13 @@ int omni_w8a16_gemm_ws(const uint16_t* x, const int8_t* w, const uint16_t* scale
 
 size_t omni_w4a16_gemm_workspace_size(int64_t rows, int64_t columns, int64_t width, int64_t group) {
     if (rows <= 0 || columns <= 0 || width <= 0 || group <= 0 || width % 32 != 0 || group % 32 != 0 ||
-        width % group != 0 || w4a16_kind(rows, columns, width) != 2)
+        width % group != 0)
         return 0;
-    return (size_t)omni::w4a16_partial_elems(rows, columns, width, group) * sizeof(float);
+    switch (w4a16_kind(rows, columns, width)) {
+        case 1: return (size_t)omni::w4a16_skinny_partial_elems(rows, columns, width) * sizeof(float);
+        case 2: return (size_t)omni::w4a16_partial_elems(rows, columns, width, group) * sizeof(float);
+        default: return 0;
+    }
 }
 
 int omni_w4a16_gemm(const uint16_t* x, const uint8_t* w_packed, const uint16_t* scale_bf16,

@@ -68,6 +68,8 @@ hipError_t launch_w4a16_mfma(const W8A16Args& a, hipStream_t stream);
 // Floats of split-K partial sums launch_w4a16_mfma uses for this shape on the
 // current device (0: no split); with fewer in W8A16Args it splits less.
 int64_t w4a16_partial_elems(int64_t rows, int64_t columns, int64_t width, int64_t group);
+// The same for launch_w4a16_skinny (up to 16 rows: split-K skinny kernel).
+int64_t w4a16_skinny_partial_elems(int64_t rows, int64_t columns, int64_t width);
 
 // fp16 linear (w8a16.hip): w is f16 [columns][width] (cast to int8_t*), no
 // scale; out[m][n] = f16(sum_k x[m][k] * w[n][k] + bias[n]).

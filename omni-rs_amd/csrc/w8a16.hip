@@ -618,9 +618,12 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_lds_kernel(W8A16Args a) {
 // K quarter w / 4 in 64-element steps, two v_mfma_f32_16x16x32_f16 per step;
 // the four quarters are added through LDS and the unit's f32 sums go to
 // partial[split][row][column], which w8a16_split_reduce_kernel adds in
-// order before scale and bias.
+// order before scale and bias. WB = 4 (W4A16): 16 codes (8 bytes) per lane
+// per step, dequantised to f16(q * s) with their group's scale, loaded
+// beside them; the reduction then adds only the bias.
 constexpr int kSkinnySplitMaxKS = 1024;
 
+template <int WB = 8>
 __global__ __launch_bounds__(1024) void w8a16_skinny_split_kernel(W8A16Args a, int splits) {
     constexpr int RS = kSkinnySplitMaxKS * 2 + 16;  // LDS bytes per x row
     constexpr int kMaxPieces = 16 * kSkinnySplitMaxKS / 8 / 1024;
@@ -654,13 +657,24 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_split_kernel(W8A16Args a, i
             xv[i] = *reinterpret_cast<const uint4*>(a.x + rowv[i] * K + k0 + 8 * colv[i]);
     }
     const int64_t wn = min(n0 + 16 * cb + r16, a.columns - 1);  // clamped: never stored
-    const uint8_t* wrow = reinterpret_cast<const uint8_t*>(a.w) + wn * K + k0 + (int64_t)kq * (KS / 4);
+    const int64_t kw = k0 + (int64_t)kq * (KS / 4);  // this wave's first k
+    const uint8_t* wrow = reinterpret_cast<const uint8_t*>(a.w) + (wn * K + kw) * WB / 8;
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
-    v4u wv[kMaxSteps];
+    v4u wv[WB == 8 ? kMaxSteps : 1];
+    typedef unsigned v2u __attribute__((ext_vector_type(2)));
+    v2u wq[WB == 4 ? kMaxSteps : 1];
+    uint16_t sq[WB == 4 ? kMaxSteps : 1];
 #pragma unroll
     for (int j = 0; j < kMaxSteps; ++j) {
         const int st = j < steps ? j : steps - 1;
-        wv[j] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wrow + 64 * st + 16 * g));
+        if constexpr (WB == 8) {
+            wv[j] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wrow + 64 * st + 16 * g));
+        } else {
+            wq[j] = __builtin_nontemporal_load(reinterpret_cast<const v2u*>(wrow + 32 * st + 8 * g));
+            // (32-bit divisions: K < 2^31 on this path)
+            sq[j] = a.gscale[wn * (int64_t)((unsigned)K / (unsigned)a.group) +
+                             (unsigned)(kw + 64 * st + 16 * g) / (unsigned)a.group];
+        }
     }
 #pragma unroll
     for (int i = 0; i < kMaxPieces; ++i)
@@ -671,10 +685,14 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_split_kernel(W8A16Args a, i
     for (int j = 0; j < kMaxSteps; ++j) {
         if (j >= steps) break;  // uniform
         v2h h[8];
-        i8x4_to_f16x4(wv[j].x, h[0], h[1]);
-        i8x4_to_f16x4(wv[j].y, h[2], h[3]);
-        i8x4_to_f16x4(wv[j].z, h[4], h[5]);
-        i8x4_to_f16x4(wv[j].w, h[6], h[7]);
+        if constexpr (WB == 8) {
+            i8x4_to_f16x4(wv[j].x, h[0], h[1]);
+            i8x4_to_f16x4(wv[j].y, h[2], h[3]);
+            i8x4_to_f16x4(wv[j].z, h[4], h[5]);
+            i8x4_to_f16x4(wv[j].w, h[6], h[7]);
+        } else {
+            i4x16_dequant(wq[j].x, wq[j].y, (_Float16)bf16_to_f32(sq[j]), h);
+        }
         const v8h b0 = v8h{h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
         const v8h b1 = v8h{h[4][0], h[4][1], h[5][0], h[5][1], h[6][0], h[6][1], h[7][0], h[7][1]};
         const uint8_t* px = sx + r16 * RS + (kq * (KS / 4) + 64 * j + 16 * g) * 2;
@@ -702,6 +720,7 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_split_kernel(W8A16Args a, i
     }
 }
 
+template <int WB = 8>
 hipError_t launch_skinny_split(const W8A16Args& a, int splits, hipStream_t stream);
 int cu_count();
 
@@ -1679,9 +1698,10 @@ __global__ __launch_bounds__(256) void w8a16_split_reduce_kernel(W8A16Args a, in
     for (int e = 0; e < e_end; ++e) a.out[i + e] = o[e];
 }
 
+template <int WB>
 hipError_t launch_skinny_split(const W8A16Args& a, int splits, hipStream_t stream) {
     const int64_t units = ((a.columns + 63) / 64) * splits;
-    hipLaunchKernelGGL(w8a16_skinny_split_kernel, dim3((unsigned)units), dim3(1024), 0, stream, a, splits);
+    hipLaunchKernelGGL((w8a16_skinny_split_kernel<WB>), dim3((unsigned)units), dim3(1024), 0, stream, a, splits);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int64_t quads = (a.rows * a.columns + 3) / 4;
@@ -1942,8 +1962,39 @@ hipError_t launch_w4a16_gemv(const W8A16Args& a, hipStream_t stream) {
     }
 }
 
+// Split count for the int4 split-K skinny kernel (1: not split): rows <= 16,
+// K / splits a multiple of 256 and at most 1024, the partial sums within the
+// workspace. By default only K of 3072..4096 split (3 or 4 ways), and only
+// where the unsplit kernel needs more than one round of 16-column
+// workgroups: MI355X, 16 x 4096 -> 14336 25.2 us split four ways against
+// 31.1, the 128256-row head 153 against 226; 8 x 2048 -> 8192 10.1 split
+// two ways against 8.5, 3584 -> 18944 (seven 512-element splits) 34.5
+// against 23.1. OMNI_W4A16_SKINNY_SPLIT=<n> pins n (0: off; test aid, read
+// on every call).
+int w4_skinny_splits(int64_t rows, int64_t width, int64_t columns, int64_t partial_elems, int cus) {
+    if (rows > 16 || width % 256 != 0 || width >= (int64_t(1) << 31)) return 1;
+    const char* v = std::getenv("OMNI_W4A16_SKINNY_SPLIT");
+    int want = v ? std::atoi(v) : -1;
+    if (want == 0) return 1;
+    if (want < 0) {
+        if (columns <= 16LL * cus || width < 3072 || width > 4 * kSkinnySplitMaxKS) return 1;
+        want = (int)((width + kSkinnySplitMaxKS - 1) / kSkinnySplitMaxKS);
+    }
+    if (want < 2 || width % (256LL * want) != 0 || width / want > kSkinnySplitMaxKS) return 1;
+    if (want * rows * columns > partial_elems) return 1;
+    return want;
+}
+
+int64_t w4a16_skinny_partial_elems(int64_t rows, int64_t columns, int64_t width) {
+    if (rows <= 0 || columns <= 0) return 0;
+    const int sp = w4_skinny_splits(rows, width, columns, INT64_MAX, cu_count());
+    return sp > 1 ? (int64_t)sp * rows * columns : 0;
+}
+
 hipError_t launch_w4a16_skinny(const W8A16Args& a, hipStream_t stream) {
     if (a.rows == 0 || a.columns == 0) return hipSuccess;
+    const int sp = w4_skinny_splits(a.rows, a.width, a.columns, a.partial ? a.partial_elems : 0, cu_count());
+    if (sp > 1) return launch_skinny_split<4>(a, sp, stream);
     const dim3 grid((unsigned)((a.columns + 15) / 16)), block(1024);
     if (a.rows <= 16) hipLaunchKernelGGL((w4a16_skinny_kernel<1>), grid, block, 0, stream, a);
     else if (a.rows <= 32) hipLaunchKernelGGL((w4a16_skinny_kernel<2>), grid, block, 0, stream, a);
