@@ -240,9 +240,10 @@ int omni_w4a16_gemm(const uint16_t* x, const uint8_t* w_packed, const uint16_t* 
                     int64_t width, uint16_t* out, void* stream);
 
 /* Bytes of workspace omni_w4a16_gemm_ws uses for this shape on the current
- * device: split-K partial sums (f32 [splits][rows][columns]) for GEMM shapes
- * (more than 64 rows) that split; 0 when the shape does not split. No
- * counterpart in the reference: it serves omni_w4a16_gemm_ws. */
+ * device: split-K partial sums (f32 [splits][rows][columns]) for the shapes
+ * that split (GEMM shapes, and 5..16 rows over long K and many columns); 0
+ * when the shape does not split. No counterpart in the reference: it
+ * serves omni_w4a16_gemm_ws. */
 size_t omni_w4a16_gemm_workspace_size(int64_t rows, int64_t columns, int64_t width, int64_t group);
 
 /* omni_w4a16_gemm with a caller-owned workspace (256-byte aligned, or NULL
