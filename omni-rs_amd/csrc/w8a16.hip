@@ -2044,9 +2044,10 @@ W4Plan plan_w4a16(const W8A16Args& a, int cus, bool ws_limited) {
     // 256..4096, K = 3584..18944: 0.02488 K' + 31.4, 0.01435 K' + 24.2,
     // 0.0107 K' + 8.1), and a split adds its reduction, 1 us + (4 splits + 2)
     // bytes per output at 3.5 TB/s; K < 4096 is not split. On seven long-K
-    // shapes it picks within 5 % of the fastest of eleven ring/split choices
-    // (1024 x 14336 -> 4096: 137-139 us split, against 166 unsplit;
-    // 1024 x 8960 -> 1536: 55 against 85).
+    // shapes its choice is within 5 % of the fastest of the ring/split
+    // choices measured on five and 13-14 % off on two (1024 x 8192 -> 4096,
+    // 1024 x 8960 -> 1536); against unsplit: 1024 x 14336 -> 4096 142 us
+    // against 182, 1024 x 8960 -> 1536 56 against 86.
     const int ktiles = (int)(a.width / 64);
     double best_t = 0.0;
     W4Plan best{5, 1};
