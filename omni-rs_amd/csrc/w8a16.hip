@@ -610,7 +610,7 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_lds_kernel(W8A16Args a) {
 }
 
 // Split-K skinny GEMM for up to 16 activation rows (int8 weights): a unit
-// is 64 columns x KS = K / splits of K (KS % 256 == 0, KS <= 1024), so each
+// is 64 columns x KS = K / splits of K (KS % 64 == 0, 256 <= KS <= 1024), so each
 // CU takes in 16 x KS x 2 bytes of x and 64 x KS bytes of weights (at
 // 16 x 4096 x 4096 and four splits: 32 KB + 64 KB, against 128 KB + 64 KB
 // for a 16-column unit over all of K). The x slice is staged into LDS as in
@@ -639,7 +639,9 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_split_kernel(W8A16Args a, i
     const int64_t n0 = (int64_t)(blockIdx.x % tiles_n) * 64;
     const int64_t k0 = (int64_t)sp * KS;
     const int cb = wave & 3, kq = wave >> 2;
-    const int steps = KS / 256;  // 64-element steps per wave
+    // The unit's KS / 64 steps of 64 elements split over the four K
+    // quarters as evenly as they go (KS >= 256: every quarter has one).
+    const int s_lo = kq * (KS / 64) / 4, steps = (kq + 1) * (KS / 64) / 4 - s_lo;
     const int r16 = lane & 15, g = lane >> 4;
     const int pieces_per_row = KS / 8;
     // Piece idx of x[0:16][k0 : k0 + KS] is 8 consecutive values; row =
@@ -657,7 +659,7 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_split_kernel(W8A16Args a, i
             xv[i] = *reinterpret_cast<const uint4*>(a.x + rowv[i] * K + k0 + 8 * colv[i]);
     }
     const int64_t wn = min(n0 + 16 * cb + r16, a.columns - 1);  // clamped: never stored
-    const int64_t kw = k0 + (int64_t)kq * (KS / 4);  // this wave's first k
+    const int64_t kw = k0 + 64 * s_lo;  // this wave's first k
     const uint8_t* wrow = reinterpret_cast<const uint8_t*>(a.w) + (wn * K + kw) * WB / 8;
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
     v4u wv[WB == 8 ? kMaxSteps : 1];
@@ -695,7 +697,7 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_split_kernel(W8A16Args a, i
         }
         const v8h b0 = v8h{h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
         const v8h b1 = v8h{h[4][0], h[4][1], h[5][0], h[5][1], h[6][0], h[6][1], h[7][0], h[7][1]};
-        const uint8_t* px = sx + r16 * RS + (kq * (KS / 4) + 64 * j + 16 * g) * 2;
+        const uint8_t* px = sx + r16 * RS + (64 * (s_lo + j) + 16 * g) * 2;
         v8h a0, a1;
         __builtin_memcpy(&a0, px, 16);
         __builtin_memcpy(&a1, px + 16, 16);
@@ -725,26 +727,28 @@ hipError_t launch_skinny_split(const W8A16Args& a, int splits, hipStream_t strea
 int cu_count();
 
 // Split count for the split-K skinny kernel (1: not split): rows <= 16, int8
-// weights, K / splits a multiple of 256 and at most 1024, and the partial
+// weights, K / splits a multiple of 64 from 256 to 1024, and the partial
 // sums fit the workspace. By default it splits only where the unsplit
-// LDS-staged kernel (16 columns per workgroup, K <= 4096) needs more than one
-// round of workgroups: measured on MI355X, 16 x 4096 -> 14336 21.7 us split
-// four ways against 25.7, 16 x 2048 -> 8192 9.4 against 10.5, but config 1
-// (16 x 4096 -> 4096, one round) 9.6 against 7.8: a single round is bound by
-// the cold fetch of x and the first weight latency, not by the x traffic the
-// split saves, and the reduction launch adds ~1.5 us.
+// LDS-staged kernel (16 columns per workgroup, K <= 4096) needs two or more
+// rounds of workgroups: measured on MI355X, 16 x 4096 -> 14336 21.7 us split
+// four ways against 25.7, 16 x 2048 -> 8192 9.4 against 10.5, 16 x 3584 ->
+// 18944 (896-element units) 24.9 against 29.3, but config 1 (16 x 4096 ->
+// 4096, one round) 9.6 against 7.8, and 8 x 3584 -> 4608 12.3 against 10.6:
+// one round is bound by the cold fetch of x and the first weight latency, not
+// by the x traffic the split saves, and the reduction launch adds ~1.5 us.
 // OMNI_W8A16_SKINNY_SPLIT=<n> pins n (0: off; test aid, read on every call).
 int skinny_splits(int64_t rows, int64_t width, int64_t columns, int64_t partial_elems, int cus) {
-    if (rows > 16 || width % 256 != 0) return 1;
+    if (rows > 16 || width % 64 != 0) return 1;
     const char* v = std::getenv("OMNI_W8A16_SKINNY_SPLIT");
     int want = v ? std::atoi(v) : -1;
     if (want == 0) return 1;
     if (want < 0) {
-        if (width > kSkinnyLdsMaxK || columns <= 16LL * cus) return 1;
+        if (width > kSkinnyLdsMaxK || columns < 32LL * cus) return 1;
         want = 1;
         while (width / want > kSkinnySplitMaxKS) want *= 2;
     }
-    if (want < 2 || width % (256LL * want) != 0 || width / want > kSkinnySplitMaxKS) return 1;
+    if (want < 2 || width % (64LL * want) != 0 || width / want < 256 || width / want > kSkinnySplitMaxKS)
+        return 1;
     if (want * rows * columns > partial_elems) return 1;
     return want;
 }
@@ -1963,24 +1967,25 @@ hipError_t launch_w4a16_gemv(const W8A16Args& a, hipStream_t stream) {
 }
 
 // Split count for the int4 split-K skinny kernel (1: not split): rows <= 16,
-// K / splits a multiple of 256 and at most 1024, the partial sums within the
+// K / splits a multiple of 64 from 256 to 1024, the partial sums within the
 // workspace. By default only K of 3072..4096 split (3 or 4 ways), and only
-// where the unsplit kernel needs more than one round of 16-column
+// where the unsplit kernel needs two or more rounds of 16-column
 // workgroups: MI355X, 16 x 4096 -> 14336 25.2 us split four ways against
-// 31.1, the 128256-row head 153 against 226; 8 x 2048 -> 8192 10.1 split
-// two ways against 8.5, 3584 -> 18944 (seven 512-element splits) 34.5
-// against 23.1. OMNI_W4A16_SKINNY_SPLIT=<n> pins n (0: off; test aid, read
+// 31.1, the 128256-row head 153 against 226, 16 x 3584 -> 18944 27.1
+// against 28.2 (8 rows: 25.2 against 23.9); 8 x 2048 -> 8192 10.1 split
+// two ways against 8.5. OMNI_W4A16_SKINNY_SPLIT=<n> pins n (0: off; test aid, read
 // on every call).
 int w4_skinny_splits(int64_t rows, int64_t width, int64_t columns, int64_t partial_elems, int cus) {
-    if (rows > 16 || width % 256 != 0 || width >= (int64_t(1) << 31)) return 1;
+    if (rows > 16 || width % 64 != 0 || width >= (int64_t(1) << 31)) return 1;
     const char* v = std::getenv("OMNI_W4A16_SKINNY_SPLIT");
     int want = v ? std::atoi(v) : -1;
     if (want == 0) return 1;
     if (want < 0) {
-        if (columns <= 16LL * cus || width < 3072 || width > 4 * kSkinnySplitMaxKS) return 1;
+        if (columns < 32LL * cus || width < 3072 || width > 4 * kSkinnySplitMaxKS) return 1;
         want = (int)((width + kSkinnySplitMaxKS - 1) / kSkinnySplitMaxKS);
     }
-    if (want < 2 || width % (256LL * want) != 0 || width / want > kSkinnySplitMaxKS) return 1;
+    if (want < 2 || width % (64LL * want) != 0 || width / want < 256 || width / want > kSkinnySplitMaxKS)
+        return 1;
     if (want * rows * columns > partial_elems) return 1;
     return want;
 }

@@ -260,12 +260,13 @@ def test_mid_rows_on_every_route(oracle, monkeypatch, route, rows, width, column
 @pytest.mark.parametrize("splits", ["auto", "2", "4"])
 @pytest.mark.parametrize("rows,width,columns,group,bias", [(16, 4096, 4200, 128, False), (9, 2048, 1000, 64, True),
                                                            (5, 4096, 300, 256, True), (12, 1024, 70, 128, False),
-                                                           (16, 3072, 4099, 128, True)])
+                                                           (16, 3072, 8199, 128, True), (7, 3584, 8300, 128, True),
+                                                           (16, 1344, 600, 64, False)])
 def test_skinny_split_k(oracle, monkeypatch, splits, rows, width, columns, group, bias):
     # The int4 split-K skinny kernel (5..16 rows): units of 64 columns x
     # K / splits, partial sums of the scaled codes added in order by the
     # reduction (bias only); forced splits, and the default choice
-    # ("auto": K of 3072..4096 over more than 4096 columns), deterministic
+    # ("auto": K of 3072..4096 over at least 8192 columns), deterministic
     if splits != "auto":
         monkeypatch.setenv("OMNI_W4A16_SKINNY_SPLIT", splits)
     rng = np.random.default_rng(rows + width + columns + group)
@@ -286,6 +287,7 @@ def test_skinny_split_k_workspace_size():
     assert L.omni_w4a16_gemm_workspace_size(16, 14336, 4096, 128) == 4 * 16 * 14336 * 4
     assert L.omni_w4a16_gemm_workspace_size(8, 8192, 3072, 128) == 3 * 8 * 8192 * 4
     assert L.omni_w4a16_gemm_workspace_size(16, 4096, 4096, 128) == 0     # one round of workgroups
-    assert L.omni_w4a16_gemm_workspace_size(16, 18944, 3584, 128) == 0    # 3584 / 4 is not a multiple of 256
+    assert L.omni_w4a16_gemm_workspace_size(16, 6144, 4096, 128) == 0     # under two rounds
+    assert L.omni_w4a16_gemm_workspace_size(16, 18944, 3584, 128) == 4 * 16 * 18944 * 4  # 896-element units
     assert L.omni_w4a16_gemm_workspace_size(16, 8192, 2048, 128) == 0     # K < 3072
     assert L.omni_w4a16_gemm_workspace_size(4, 14336, 4096, 128) == 0     # GEMV

@@ -271,7 +271,8 @@ def test_split_k_workspace_contract(monkeypatch):
 @pytest.mark.parametrize("splits", ["auto", "2", "4", "8"])
 @pytest.mark.parametrize("rows,width,columns,bias", [(16, 4096, 4096, False), (9, 2048, 1000, True),
                                                      (5, 8192, 300, True), (12, 256, 70, False),
-                                                     (16, 1024, 4099, True), (13, 12288, 128, False)])
+                                                     (16, 1024, 4099, True), (13, 12288, 128, False),
+                                                     (16, 3584, 8300, True), (8, 1344, 600, False)])
 def test_skinny_split_k(oracle, monkeypatch, splits, rows, width, columns, bias):
     # The decode-shaped split-K kernel (5..16 rows): units of 64 columns x
     # K / splits, f32 partial sums, then the in-order reduction. Splits that
@@ -301,7 +302,8 @@ def test_skinny_split_k_workspace_size():
     assert L.omni_w8a16_gemm_workspace_size(16, 8192, 2048) == 2 * 16 * 8192 * 4
     assert L.omni_w8a16_gemm_workspace_size(16, 4096, 4096) == 0                   # config 1: one round
     assert L.omni_w8a16_gemm_workspace_size(16, 8192, 1024) == 0                   # K fits one unit
-    assert L.omni_w8a16_gemm_workspace_size(16, 8192, 4160) == 0                   # K % 256 != 0
+    assert L.omni_w8a16_gemm_workspace_size(16, 8192, 4160) == 0                   # K > 4096
+    assert L.omni_w8a16_gemm_workspace_size(16, 18944, 3584) == 4 * 16 * 18944 * 4  # 896-element units
     assert L.omni_w8a16_gemm_workspace_size(16, 8192, 8192) == 0                   # K > 4096
     assert L.omni_w8a16_gemm_workspace_size(17, 4096, 4096) == 0                   # skinny, not split
     # 17 rows of a 58.7 M-weight matrix take the GEMM, split K (64 x 128 tiles)
