@@ -103,7 +103,8 @@ def test_gemv_every_configuration(oracle, monkeypatch, cfg):
 
 @pytest.mark.parametrize("rows,k,n", [(5, 96, 65), (17, 1024, 256), (33, 4096, 1000),
                                       (64, 8192, 4096), (48, 40960, 33), (2, 40960, 50),
-                                      (8, 1024, 256), (16, 4096, 1000), (12, 2048, 64)])
+                                      (8, 1024, 256), (16, 4096, 1000), (12, 2048, 64),
+                                      (6, 3072, 130)])
 def test_skinny_rows(oracle, rows, k, n):
     # 5..64 rows (and rows past the GEMV's widest row) run the skinny MFMA kernel.
     rng = np.random.default_rng(rows * 7 + k + n)

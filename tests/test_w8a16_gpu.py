@@ -147,11 +147,13 @@ def test_skinny_rows_on_both_routes(oracle, monkeypatch, route, rows, width, col
 
 @pytest.mark.parametrize("kernel", ["0", "1"])
 @pytest.mark.parametrize("rows,width,columns", [(5, 64, 33), (8, 960, 70), (16, 4096, 4096),
-                                                (13, 2048, 17), (16, 4096, 129), (11, 4032, 300)])
+                                                (13, 2048, 17), (16, 4096, 129), (11, 4032, 300),
+                                                (7, 1024, 50), (14, 3072, 101), (16, 3136, 64)])
 def test_skinny_lds_kernel_and_fallback(oracle, monkeypatch, kernel, rows, width, columns):
     # 5..16 rows with K % 64 == 0 and K <= 4096: the LDS-staged skinny kernel
-    # (0) and w8a16_skinny_kernel (OMNI_W8A16_SKINNY=1), with idle waves
-    # (K < 1024), ragged column counts and bias, against the f64 truth.
+    # (0; its K = 1024 / 2048 / 3072 / 4096 builds and the run-time-K one) and
+    # w8a16_skinny_kernel (OMNI_W8A16_SKINNY=1), with idle waves (K < 1024),
+    # ragged column counts and bias, against the f64 truth.
     monkeypatch.setenv("OMNI_W8A16_SKINNY", kernel)
     rng = np.random.default_rng(rows * 5 + width + columns)
     x, w, s, b = make(rng, rows, width, columns, bias=True)
