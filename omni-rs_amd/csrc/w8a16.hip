@@ -180,7 +180,10 @@ __device__ __forceinline__ int fold_index(int lane) {
 // folded, so each x chunk held in registers serves R * B weight rows (x is
 // read from L2 once per workgroup: 2 * MR bytes per weight byte / (R * B)).
 // WB = 16: f16 weights, no scale (the fp16 linear).
-template <int MR, int CPL, int R, int WB = 8, int B = 1>
+// KF > 0 builds the kernel for K == KF with the workgroup size the launcher
+// derives from it: where the lanes' chunks cover the row exactly, no chunk
+// index is clamped or checked.
+template <int MR, int CPL, int R, int WB = 8, int B = 1, int KF = 0>
 __global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
     constexpr int V = R * MR;
     constexpr int RB = R * B;
@@ -188,12 +191,15 @@ __global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
     static_assert(WB == 8 || WB == 16, "int8 or f16 weights");
     constexpr int kE = WB == 8 ? 16 : 8;  // weights per 16-byte chunk
     constexpr int kP = kE / 2;            // f16 pairs of x per chunk
+    constexpr int kChunks = KF / kE;
+    constexpr int kT = ((kChunks + CPL - 1) / CPL + 63) / 64 * 64;  // the launcher's workgroup size for KF
+    constexpr bool kExact = KF > 0 && kT * CPL == kChunks;          // every chunk index in range
     __shared__ float s_part[16][B * V];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int T = blockDim.x;
-    const int64_t K = a.width;
+    const int T = KF > 0 ? kT : (int)blockDim.x;
+    const int64_t K = KF > 0 ? KF : a.width;
     const int64_t chunks = K / kE;
     const int64_t n0 = (int64_t)blockIdx.x * RB;
 
@@ -204,7 +210,7 @@ __global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
         const int64_t c = tid + (int64_t)T * j;
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-            if (c < chunks && m < a.rows) {
+            if ((kExact || c < chunks) && (MR == 1 || m < a.rows)) {  // rows >= 1
                 const uint4* p = reinterpret_cast<const uint4*>(a.x + m * K + c * kE);
 #pragma unroll
                 for (int u = 0; u < kE / 8; ++u) {
@@ -251,7 +257,7 @@ __global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
         const uint8_t* wrow = reinterpret_cast<const uint8_t*>(a.w) + n * K * (WB / 8);
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-            const int64_t c = tid + (int64_t)T * j < chunks ? tid + (int64_t)T * j : chunks - 1;
+            const int64_t c = kExact || tid + (int64_t)T * j < chunks ? tid + (int64_t)T * j : chunks - 1;
             wv[r][j] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wrow + c * 16));
         }
     }
@@ -331,16 +337,28 @@ int gemv_cfg_override(int wb) {
     return v ? std::atoi(v) : 0;
 }
 
-template <int MR, int CPL, int R, int WB, int B = 1>
+template <int MR, int CPL, int R, int WB, int B = 1, int KF = 0>
 hipError_t launch_gemv_cfg(const W8A16Args& a, hipStream_t stream) {
+    if (KF > 0 && a.width != KF) return hipErrorInvalidValue;
     const int64_t chunks = a.width / (WB == 8 ? 16 : 8);
     const int64_t lanes = (chunks + CPL - 1) / CPL;
     const int64_t T = ((lanes + 63) / 64) * 64;
     if (T > 1024) return hipErrorInvalidValue;  // the caller bounds width
     const int64_t grid = (a.columns + R * B - 1) / (R * B);
-    hipLaunchKernelGGL((w8a16_gemv_kernel<MR, CPL, R, WB, B>), dim3((unsigned)grid), dim3((unsigned)T), 0,
+    hipLaunchKernelGGL((w8a16_gemv_kernel<MR, CPL, R, WB, B, KF>), dim3((unsigned)grid), dim3((unsigned)T), 0,
                        stream, a);
     return hipGetLastError();
+}
+
+// One-row int8 decode at the widths of the benchmarked models' linears
+// (4096, 14336) runs the kernel built for that K.
+template <int MR, int CPL, int R, int WB, int B = 1>
+hipError_t launch_gemv_k(const W8A16Args& a, hipStream_t stream) {
+    if constexpr (MR == 1 && WB == 8) {
+        if (a.width == 4096) return launch_gemv_cfg<MR, CPL, R, WB, B, 4096>(a, stream);
+        if (a.width == 14336) return launch_gemv_cfg<MR, CPL, R, WB, B, 14336>(a, stream);
+    }
+    return launch_gemv_cfg<MR, CPL, R, WB, B>(a, stream);
 }
 
 template <int MR, int WB>
@@ -380,12 +398,12 @@ hipError_t launch_gemv_m(const W8A16Args& a, hipStream_t stream) {
     // 512 chunks and 64 M weights (17 % faster than batches of 8 at
     // 4096 x 4096, 5 % at 4096 x 14336), batches of 8 beyond (the 128256-row
     // head, K = 14336).
-    if (a.columns * a.width <= (4 << 20)) return launch_gemv_cfg<MR, 2, 1, WB>(a, stream);
+    if (a.columns * a.width <= (4 << 20)) return launch_gemv_k<MR, 2, 1, WB>(a, stream);
     if (MR == 4 && chunks <= 512 && a.columns * a.width <= (64 << 20))
         return launch_gemv_cfg<MR, 1, 4, WB, 2>(a, stream);
     if (MR == 4 && chunks <= 1024) return launch_gemv_cfg<MR, 1, 8, WB, 2>(a, stream);
-    if (chunks > 512) return launch_gemv_cfg<MR, 2, 4, WB>(a, stream);
-    return launch_gemv_cfg<MR, 1, 4, WB>(a, stream);
+    if (chunks > 512) return launch_gemv_k<MR, 2, 4, WB>(a, stream);
+    return launch_gemv_k<MR, 1, 4, WB>(a, stream);
 }
 
 // ---------------------------------------------------------------------------
