@@ -829,21 +829,25 @@ hipError_t launch_skinny(const W8A16Args& a, hipStream_t stream) {
 // are exact and the f32 sums stay below 2^13 * sum|x|, so the correction
 // costs ~1e-4 of the result relative and nothing on integer data. A
 // workgroup of T = 64 * ceil(K / 2048) lanes owns R weight rows; every weight
-// load is issued up front.
-template <int MR, int R, int B = 1>
+// load is issued up front. KF > 0 and GF > 0 build the kernel for K == KF,
+// a multiple of 2048 (every lane then owns one chunk), and group == GF: no
+// clamp, and the scale index without a 64-bit division.
+template <int MR, int R, int B = 1, int KF = 0, int GF = 0>
 __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W8A16Args a) {
     constexpr int V = R * MR;
     constexpr int RB = R * B;  // rows per workgroup: B batches of R
     static_assert((V & (V - 1)) == 0 && V <= 64, "power-of-two partial count");
+    static_assert(KF % 2048 == 0 && (KF == 0) == (GF == 0), "KF: a multiple of 2048, with GF");
     __shared__ float s_part[16][B * V];
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int T = blockDim.x;
-    const int64_t K = a.width;
+    const int T = KF > 0 ? KF / 32 : (int)blockDim.x;
+    const int64_t K = KF > 0 ? KF : a.width;
+    const int64_t group = GF > 0 ? GF : a.group;
     const int64_t chunks = K / 32;
-    const int64_t gpr = K / a.group;  // scale groups per weight row
+    const int64_t gpr = K / group;  // scale groups per weight row
     const int64_t n0 = (int64_t)blockIdx.x * RB;
-    const bool live = tid < chunks;
+    const bool live = KF > 0 || tid < chunks;
     const int64_t c = live ? tid : chunks - 1;  // clamped: meets zero activations
 
     // x: 32 halves of each row's chunk as 16 f16 pairs, in the order of
@@ -895,7 +899,7 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W8A16Args a) {
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
         const int64_t n = n0 + r < a.columns ? n0 + r : a.columns - 1;
-        sc[r] = bf16_to_f32(a.gscale[n * gpr + (c * 32) / a.group]);
+        sc[r] = bf16_to_f32(a.gscale[n * gpr + (c * 32) / group]);
     }
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
@@ -1978,6 +1982,18 @@ hipError_t launch_w4a16_gemv(const W8A16Args& a, hipStream_t stream) {
     auto go = [&](auto rt, auto bt) {
         constexpr int R = decltype(rt)::value, B = decltype(bt)::value;
         const dim3 grid((unsigned)((a.columns + R * B - 1) / (R * B))), block((unsigned)T);
+        // One-row decode at the benchmarked models' widths and group 128
+        // runs the kernel built for them.
+        if (a.rows == 1 && a.group == 128) {
+            if (a.width == 4096) {
+                hipLaunchKernelGGL((w4a16_gemv_kernel<1, R, B, 4096, 128>), grid, block, 0, stream, a);
+                return hipGetLastError();
+            }
+            if (a.width == 14336) {
+                hipLaunchKernelGGL((w4a16_gemv_kernel<1, R, B, 14336, 128>), grid, block, 0, stream, a);
+                return hipGetLastError();
+            }
+        }
         switch (a.rows) {
             case 1: hipLaunchKernelGGL((w4a16_gemv_kernel<1, R, B>), grid, block, 0, stream, a); break;
             case 2: hipLaunchKernelGGL((w4a16_gemv_kernel<2, R, B>), grid, block, 0, stream, a); break;

@@ -51,7 +51,7 @@ def test_reference_synthetic_case(oracle, out, input, m):
 
 @pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 16, 33, 64, 65, 300])
 @pytest.mark.parametrize("width,columns,group", [(2048, 512, 128), (512, 2048, 128), (4096, 77, 128),
-                                                 (1536, 130, 64), (96, 9, 32)])
+                                                 (1536, 130, 64), (96, 9, 32), (14336, 40, 128)])
 def test_every_path_random(oracle, rows, width, columns, group):
     rng = np.random.default_rng(rows * 7 + width + columns + group)
     x, packed, bits, b = wd.random_case(rng, rows, width, columns, group, bias=columns % 2 == 1)
@@ -65,13 +65,16 @@ def test_every_path_random(oracle, rows, width, columns, group):
 @pytest.mark.parametrize("r", ["11", "21", "41", "81", "42", "44", "82"])
 def test_gemv_every_rows_per_workgroup(oracle, monkeypatch, r):
     # OMNI_W4A16_GEMV=<rows per batch><batches per workgroup>; column counts
-    # leave the last workgroup's batches partly or wholly past the matrix
+    # leave the last workgroup's batches partly or wholly past the matrix;
+    # one row at K = 4096 / 14336 with group 128 runs the kernels built for
+    # those shapes
     monkeypatch.setenv("OMNI_W4A16_GEMV", r)
-    for rows, width, columns in ((1, 4096, 37), (4, 2048, 130), (3, 96, 9)):
+    for rows, width, columns, group in ((1, 4096, 37, 32), (4, 2048, 130, 32), (3, 96, 9, 32),
+                                        (1, 4096, 37, 128), (1, 14336, 21, 128)):
         rng = np.random.default_rng(rows + width + columns + int(r))
-        x, packed, bits, b = wd.random_case(rng, rows, width, columns, 32, bias=True)
-        got = run(x, packed, bits, b, 32).astype(np.float64)
-        truth = oracle.w4a16_f64(x, packed, bits, 32, b)
+        x, packed, bits, b = wd.random_case(rng, rows, width, columns, group, bias=True)
+        got = run(x, packed, bits, b, group).astype(np.float64)
+        truth = oracle.w4a16_f64(x, packed, bits, group, b)
         assert tolerance.rel_err(got, truth) <= tolerance.FP16_REL_TOL, (r, rows, width, columns)
 
 
