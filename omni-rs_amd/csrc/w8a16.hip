@@ -350,13 +350,17 @@ hipError_t launch_gemv_cfg(const W8A16Args& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// One-row int8 decode at the widths of the benchmarked models' linears
-// (4096, 14336) runs the kernel built for that K.
+// One-row decode at the widths of the benchmarked models' linears (int8:
+// 4096, 14336; f16: the 8192-wide depth GEMV) runs the kernel built for
+// that K.
 template <int MR, int CPL, int R, int WB, int B = 1>
 hipError_t launch_gemv_k(const W8A16Args& a, hipStream_t stream) {
     if constexpr (MR == 1 && WB == 8) {
         if (a.width == 4096) return launch_gemv_cfg<MR, CPL, R, WB, B, 4096>(a, stream);
         if (a.width == 14336) return launch_gemv_cfg<MR, CPL, R, WB, B, 14336>(a, stream);
+    }
+    if constexpr (MR == 1 && WB == 16) {
+        if (a.width == 8192) return launch_gemv_cfg<MR, CPL, R, WB, B, 8192>(a, stream);
     }
     return launch_gemv_cfg<MR, CPL, R, WB, B>(a, stream);
 }
@@ -388,7 +392,7 @@ hipError_t launch_gemv_m(const W8A16Args& a, hipStream_t stream) {
         if (chunks > 1024) return launch_gemv_cfg<MR, 2, 2, WB>(a, stream);
         if (a.columns * a.width * 2 <= (4 << 20)) return launch_gemv_cfg<MR, 1, 2, WB>(a, stream);
         if (MR == 4) return launch_gemv_cfg<MR, 1, 8, WB>(a, stream);
-        return launch_gemv_cfg<MR, 1, 4, WB>(a, stream);
+        return launch_gemv_k<MR, 1, 4, WB>(a, stream);
     }
     // Measured on MI355X over the BASELINE decode shapes: 64 bytes of weights
     // in flight per lane, two chunks per lane once a row is wider than 512
