@@ -351,13 +351,15 @@ hipError_t launch_gemv_cfg(const W8A16Args& a, hipStream_t stream) {
 }
 
 // One-row decode at the widths of the benchmarked models' linears (int8:
-// 4096, 14336; f16: the 8192-wide depth GEMV) runs the kernel built for
-// that K.
+// 4096, 14336 and the small VLM's 1536, 8960; f16: the 8192-wide depth
+// GEMV) runs the kernel built for that K.
 template <int MR, int CPL, int R, int WB, int B = 1>
 hipError_t launch_gemv_k(const W8A16Args& a, hipStream_t stream) {
     if constexpr (MR == 1 && WB == 8) {
         if (a.width == 4096) return launch_gemv_cfg<MR, CPL, R, WB, B, 4096>(a, stream);
         if (a.width == 14336) return launch_gemv_cfg<MR, CPL, R, WB, B, 14336>(a, stream);
+        if (a.width == 1536) return launch_gemv_cfg<MR, CPL, R, WB, B, 1536>(a, stream);
+        if (a.width == 8960) return launch_gemv_cfg<MR, CPL, R, WB, B, 8960>(a, stream);
     }
     if constexpr (MR == 1 && WB == 16) {
         if (a.width == 8192) return launch_gemv_cfg<MR, CPL, R, WB, B, 8192>(a, stream);

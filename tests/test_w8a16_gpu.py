@@ -82,6 +82,19 @@ def test_gemv_every_configuration(oracle, monkeypatch, cfg):
         assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL, (cfg, rows, width, columns)
 
 
+@pytest.mark.parametrize("width,columns", [(4096, 4099), (14336, 4097), (1536, 8963), (8960, 1539),
+                                          (1536, 515), (4096, 1027)])
+def test_gemv_k_builds_ragged_columns(oracle, width, columns):
+    # One row at K = 4096 / 14336 / 1536 / 8960 runs the GEMV built for that
+    # K (one, two or four rows per workgroup by matrix size); column counts
+    # leave the last workgroup partly past the matrix.
+    rng = np.random.default_rng(width + columns)
+    x, w, s, b = make(rng, 1, width, columns, bias=True)
+    got = host(oi.w8a16_linear(dev(x), dev(w), dev(s), dev(b)))
+    ref = oracle.w8a16_f64(x, w, s, b)
+    assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL, (width, columns)
+
+
 def test_gemv_exact_on_integer_inputs():
     # integer x, scale 1: every partial sum is an integer below 2^11 -> exact
     x = np.tile(np.arange(-4, 4, dtype=np.float16), (4, 64))[:, :512].copy()
