@@ -70,30 +70,48 @@ __device__ __forceinline__ float block_max(float v, float* s_red) {
     return fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
 }
 
-// Single-read variant: each thread owns chunks tid + 256*j (j < CPT) of 16
-// elements, held in registers between the peak and the code pass.
-template <typename T, int CPT>
+// The same over NW waves of one workgroup.
+template <int NW>
+__device__ __forceinline__ float block_max_n(float v, float* s_red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    v = wave_max(v);
+    if (lane == 0) s_red[wave] = v;
+    __syncthreads();
+    float m = s_red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) m = fmaxf(m, s_red[w]);
+    return m;
+}
+
+// Single-read variant: each of the TPB threads owns chunks tid + TPB*j
+// (j < CPT) of 16 elements, held in registers between the peak and the code
+// pass. KF > 0 builds it for width == KF == 16 * TPB * CPT: every chunk
+// index is in range, with no predicate.
+template <typename T, int CPT, int KF = 0, int TPB = 256>
 __global__ __launch_bounds__(256) void quantize_rows_reg_kernel(
     const T* __restrict__ x, int64_t width, int64_t ld, uint8_t* __restrict__ codes,
     float* __restrict__ scale_out, int32_t* __restrict__ sum_out) {
-    __shared__ float s_peak[4];
-    __shared__ int s_sum[4];
+    static_assert(TPB % 64 == 0 && TPB <= 256, "whole waves, at most four");
+    static_assert(KF == 0 || KF == 16 * TPB * CPT, "KF covers the lanes exactly");
+    constexpr int NW = TPB / 64;
+    __shared__ float s_peak[NW];
+    __shared__ int s_sum[NW];
     const int64_t row = blockIdx.x;
     const int tid = threadIdx.x;
     const T* src = x + row * ld;
-    const int chunks = (int)(width / 16);
+    const int chunks = KF > 0 ? KF / 16 : (int)(width / 16);
     float v[CPT][16];
     float peak = 0.0f;
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
-        const int c = tid + 256 * j;
-        if (c < chunks) {
+        const int c = tid + TPB * j;
+        if (KF > 0 || c < chunks) {
             load_row_chunk<T, 16, true>(src + (int64_t)c * 16, v[j]);
 #pragma unroll
             for (int i = 0; i < 16; ++i) peak = fmaxf(peak, __builtin_fabsf(v[j][i]));
         }
     }
-    peak = block_max(peak, s_peak);
+    peak = block_max_n<NW>(peak, s_peak);
     const float s = row_scale_of(peak);
     const float y = 1.0f / s;
     const bool tiny = s < 0x1p-90f;
@@ -103,8 +121,8 @@ __global__ __launch_bounds__(256) void quantize_rows_reg_kernel(
         constexpr bool kTiny = decltype(tiny_tag)::value;
 #pragma unroll
         for (int j = 0; j < CPT; ++j) {
-            const int c = tid + 256 * j;
-            if (c < chunks) {
+            const int c = tid + TPB * j;
+            if (KF > 0 || c < chunks) {
                 uint4 w;
                 w.x = pack4<kTiny>(&v[j][0], s, y, local);
                 w.y = pack4<kTiny>(&v[j][4], s, y, local);
@@ -119,7 +137,12 @@ __global__ __launch_bounds__(256) void quantize_rows_reg_kernel(
         local = wave_sum_i32(local);
         if ((tid & 63) == 0) s_sum[tid >> 6] = local;
         __syncthreads();
-        if (tid == 0) sum_out[row] = s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3];
+        if (tid == 0) {
+            int total = 0;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) total += s_sum[w];
+            sum_out[row] = total;
+        }
     }
     if (tid == 0) scale_out[row] = s;
 }
@@ -292,6 +315,18 @@ hipError_t launch_typed(const T* x, int64_t rows, int64_t width, int64_t ld, uin
     if (width % 16 == 0 && width <= 16384 && aligned_for(16)) {
         const int cpt = (int)((width / 16 + 255) / 256);
         dim3 grid((unsigned)rows), block(256);
+        // The bench model's widths, built with every lane owning whole
+        // chunks (3072: three waves of one chunk, not four with one idle).
+        if (width == 3072) {
+            hipLaunchKernelGGL((quantize_rows_reg_kernel<T, 1, 3072, 192>), grid, dim3(192), 0, stream, x, width, ld,
+                               codes, scale, sum);
+            return hipGetLastError();
+        }
+        if (width == 12288) {
+            hipLaunchKernelGGL((quantize_rows_reg_kernel<T, 3, 12288, 256>), grid, block, 0, stream, x, width, ld,
+                               codes, scale, sum);
+            return hipGetLastError();
+        }
         switch (cpt) {
             case 1: hipLaunchKernelGGL((quantize_rows_reg_kernel<T, 1>), grid, block, 0, stream, x, width, ld, codes, scale, sum); break;
             case 2: hipLaunchKernelGGL((quantize_rows_reg_kernel<T, 2>), grid, block, 0, stream, x, width, ld, codes, scale, sum); break;
