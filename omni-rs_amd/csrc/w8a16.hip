@@ -654,8 +654,12 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_lds_kernel(W8A16Args a) {
 // beside them; the reduction then adds only the bias.
 constexpr int kSkinnySplitMaxKS = 1024;
 
-template <int WB = 8>
+// KSF > 0 builds the kernel for units of exactly KSF = 1024 values of K:
+// every wave then has four steps and every lane two x pieces, with no range
+// check.
+template <int WB = 8, int KSF = 0>
 __global__ __launch_bounds__(1024) void w8a16_skinny_split_kernel(W8A16Args a, int splits) {
+    static_assert(KSF == 0 || KSF == kSkinnySplitMaxKS, "KSF: the whole unit size");
     constexpr int RS = kSkinnySplitMaxKS * 2 + 16;  // LDS bytes per x row
     constexpr int kMaxPieces = 16 * kSkinnySplitMaxKS / 8 / 1024;
     constexpr int kMaxSteps = kSkinnySplitMaxKS / 4 / 64;
@@ -664,7 +668,7 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_split_kernel(W8A16Args a, i
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int64_t K = a.width;
-    const int KS = (int)(K / splits);
+    const int KS = KSF > 0 ? KSF : (int)(K / splits);
     const int tiles_n = (int)((a.columns + 63) / 64);
     const int sp = (int)(blockIdx.x / tiles_n);
     const int64_t n0 = (int64_t)(blockIdx.x % tiles_n) * 64;
@@ -672,7 +676,7 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_split_kernel(W8A16Args a, i
     const int cb = wave & 3, kq = wave >> 2;
     // The unit's KS / 64 steps of 64 elements split over the four K
     // quarters as evenly as they go (KS >= 256: every quarter has one).
-    const int s_lo = kq * (KS / 64) / 4, steps = (kq + 1) * (KS / 64) / 4 - s_lo;
+    const int s_lo = kq * (KS / 64) / 4, steps = KSF > 0 ? KSF / 256 : (kq + 1) * (KS / 64) / 4 - s_lo;
     const int r16 = lane & 15, g = lane >> 4;
     const int pieces_per_row = KS / 8;
     // Piece idx of x[0:16][k0 : k0 + KS] is 8 consecutive values; row =
@@ -683,10 +687,10 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_split_kernel(W8A16Args a, i
 #pragma unroll
     for (int i = 0; i < kMaxPieces; ++i) {
         const int idx = i * 1024 + tid;
-        rowv[i] = (int)(((float)idx + 0.5f) * inv_ppr);
+        rowv[i] = KSF > 0 ? idx / (KSF / 8) : (int)(((float)idx + 0.5f) * inv_ppr);
         colv[i] = idx - rowv[i] * pieces_per_row;
         xv[i] = make_uint4(0, 0, 0, 0);
-        if (rowv[i] < 16 && rowv[i] < a.rows)
+        if ((KSF > 0 || rowv[i] < 16) && rowv[i] < a.rows)
             xv[i] = *reinterpret_cast<const uint4*>(a.x + rowv[i] * K + k0 + 8 * colv[i]);
     }
     const int64_t wn = min(n0 + 16 * cb + r16, a.columns - 1);  // clamped: never stored
@@ -699,7 +703,7 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_split_kernel(W8A16Args a, i
     uint16_t sq[WB == 4 ? kMaxSteps : 1];
 #pragma unroll
     for (int j = 0; j < kMaxSteps; ++j) {
-        const int st = j < steps ? j : steps - 1;
+        const int st = KSF > 0 || j < steps ? j : steps - 1;
         if constexpr (WB == 8) {
             wv[j] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wrow + 64 * st + 16 * g));
         } else {
@@ -711,12 +715,12 @@ __global__ __launch_bounds__(1024) void w8a16_skinny_split_kernel(W8A16Args a, i
     }
 #pragma unroll
     for (int i = 0; i < kMaxPieces; ++i)
-        if (rowv[i] < 16) *reinterpret_cast<uint4*>(sx + rowv[i] * RS + colv[i] * 16) = xv[i];
+        if (KSF > 0 || rowv[i] < 16) *reinterpret_cast<uint4*>(sx + rowv[i] * RS + colv[i] * 16) = xv[i];
     __syncthreads();
     v4f_t acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int j = 0; j < kMaxSteps; ++j) {
-        if (j >= steps) break;  // uniform
+        if (KSF == 0 && j >= steps) break;  // uniform
         v2h h[8];
         if constexpr (WB == 8) {
             i8x4_to_f16x4(wv[j].x, h[0], h[1]);
@@ -1746,7 +1750,11 @@ __global__ __launch_bounds__(256) void w8a16_split_reduce_kernel(W8A16Args a, in
 template <int WB>
 hipError_t launch_skinny_split(const W8A16Args& a, int splits, hipStream_t stream) {
     const int64_t units = ((a.columns + 63) / 64) * splits;
-    hipLaunchKernelGGL((w8a16_skinny_split_kernel<WB>), dim3((unsigned)units), dim3(1024), 0, stream, a, splits);
+    if (a.width == (int64_t)kSkinnySplitMaxKS * splits)
+        hipLaunchKernelGGL((w8a16_skinny_split_kernel<WB, kSkinnySplitMaxKS>), dim3((unsigned)units), dim3(1024), 0,
+                           stream, a, splits);
+    else
+        hipLaunchKernelGGL((w8a16_skinny_split_kernel<WB>), dim3((unsigned)units), dim3(1024), 0, stream, a, splits);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int64_t quads = (a.rows * a.columns + 3) / 4;
