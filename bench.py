@@ -229,11 +229,17 @@ def step_parity(oracle, np, torch, cases, step_outs, rows_per_shape=6):
 def reference_shape_context(torch, oi, dev, stream, steps):
     """The reference's own published int8 GEMM shapes (m x n x k = 256 x
     4096 x 4096, 256 x 12288 x 4096, 256 x 4096 x 12288; its matmul2d on an
-    Apple M5 Max: 0.171 / 0.943 / 0.595 ms, int32 out) on this GPU's W8A8
-    GEMM (f32 out, fused epilogue), on the reference's own deterministic
-    operands (scripts/bench_qwen_tensorops_int8.mm:46-47), with its sampled
-    int32-dot exactness check (:65-79) on the accumulators. Cross-hardware
-    context only: different chips, and this GEMM also applies the epilogue."""
+    Apple M5 Max: 0.171 / 0.943 / 0.595 ms, int32 out), timed through the
+    reference operator try_int8_gemm (quantisation of the f16 activations +
+    the W8A8 GEMM, f32 out) with the split-K workspace (``us``), with the
+    plain workspace (``unsplit_us``: no split) and the GEMM alone on the
+    codes (``gemm_us``), on the reference's own deterministic operands
+    (scripts/bench_qwen_tensorops_int8.mm:46-47) as f16 activations and int8
+    weights, with its sampled int32-dot exactness check (:65-79) on the
+    accumulators. Cross-hardware context only: different chips, and this
+    operator also quantises and applies the epilogue."""
+    from omni_int8 import _lib
+    L = _lib.lib()
     res = []
     for m, n, k, m5_ms in ((256, 4096, 4096, 0.171), (256, 12288, 4096, 0.943),
                            (256, 4096, 12288, 0.595)):
@@ -241,19 +247,33 @@ def reference_shape_context(torch, oi, dev, stream, steps):
         b = ((torch.arange(n * k, device=dev, dtype=torch.int64) * 17 + 3) % 241 - 120)
         a = a.to(torch.int8).reshape(m, k)
         b = b.to(torch.int8).reshape(n, k)
-        rs = torch.ones(m, device=dev)
+        x = a.to(torch.float16)
+        wp = b.view(torch.int32).reshape(-1)
         ws = torch.ones(n, device=dev)
+        zero = torch.zeros(n, dtype=torch.int32, device=dev)
+        out = torch.empty((m, n), dtype=torch.float32, device=dev)
+        split_bytes = L.omni_try_int8_gemm_split_workspace_size(m, n, k)
+        plain_bytes = L.omni_try_int8_gemm_workspace_size(m, k)
+        work = {nb: torch.empty(nb, dtype=torch.uint8, device=dev) for nb in {split_bytes, plain_bytes}}
+        codes = oi.quantize_rows(x)
 
-        def one():
-            oi.w8a8_gemm(a, rs, None, b, ws)
+        def op(nbytes):
+            st = L.omni_try_int8_gemm(x.data_ptr(), oi.OMNI_F16, m, k, wp.data_ptr(), wp.numel(), ws.data_ptr(),
+                                      n, zero.data_ptr(), n, out.data_ptr(), work[nbytes].data_ptr(), nbytes,
+                                      torch.cuda.current_stream(dev).cuda_stream)
+            assert st == 0, _lib.last_error()
 
-        mark(torch, f"ref_{m}x{n}x{k}")
-        for _ in range(3):
-            one()
-        g = graph_of(one, steps)
-        t = timed_graph(g, stream) / steps
-        del g
-        _, acc = oi.w8a8_gemm(a, rs, None, b, ws, acc_dump=True)
+        times = {}
+        for name, fn in (("us", lambda: op(split_bytes)), ("unsplit_us", lambda: op(plain_bytes)),
+                         ("gemm_us", lambda: oi.w8a8_gemm(codes[0], codes[1], codes[2], b, ws, zero))):
+            mark(torch, f"ref_{m}x{n}x{k}_{name}")
+            for _ in range(3):
+                fn()
+            g = graph_of(fn, steps)
+            times[name] = timed_graph(g, stream) / steps
+            del g
+        t = times["us"]
+        _, acc = oi.w8a8_gemm(a, torch.ones(m, device=dev), None, b, ws, acc_dump=True)
         torch.cuda.synchronize()
         worst = 0
         for sidx in range(32):
@@ -264,9 +284,13 @@ def reference_shape_context(torch, oi, dev, stream, steps):
         del acc
         res.append({"m": m, "n": n, "k": k, "us": round(t * 1e6, 2),
                     "TOPS": round(2.0 * m * n * k / t / 1e12, 1),
+                    "unsplit_us": round(times["unsplit_us"] * 1e6, 2),
+                    "gemm_us": round(times["gemm_us"] * 1e6, 2),
+                    "split": bool(split_bytes > plain_bytes),
                     "sampled_dot_max_abs_err": worst,
                     "reference_m5max_matmul2d_ms": m5_ms,
-                    "note": "cross-hardware context (Apple M5 Max, int32 out, no epilogue)"})
+                    "note": "try_int8_gemm incl. quantisation; cross-hardware context "
+                            "(Apple M5 Max, int32 out, no epilogue)"})
     return res
 
 

@@ -113,9 +113,12 @@ size_t omni_w8a8_gemm_workspace_size(int64_t rows, int64_t columns, int64_t widt
 
 /* omni_w8a8_gemm with a caller-owned workspace (256-byte aligned, or NULL
  * with workspace_bytes 0), which lets the MFMA GEMM split K across
- * workgroups; with less than omni_w8a8_gemm_workspace_size bytes it splits
- * less, with none it runs as omni_w8a8_gemm. The int32 partial sums add
- * exactly, so outputs (and acc_dump) are bit-identical to omni_w8a8_gemm's. */
+ * workgroups (a second launch adds the partial sums and applies the
+ * epilogue); with less than omni_w8a8_gemm_workspace_size bytes it splits
+ * less, with none it runs as omni_w8a8_gemm. The workspace needs no
+ * initialisation; calls that overlap in time must not share one. The int32
+ * partial sums add exactly, so outputs (and acc_dump) are bit-identical to
+ * omni_w8a8_gemm's. */
 int omni_w8a8_gemm_ws(const int32_t* x_packed, const float* x_scale, const int32_t* x_sum,
                       const int32_t* w_packed, const float* w_scale, const int32_t* w_zero,
                       const float* bias, int64_t rows, int64_t columns, int64_t width, void* out,
@@ -126,12 +129,25 @@ int omni_w8a8_gemm_ws(const int32_t* x_packed, const float* x_scale, const int32
  * (codes, row scales and row sums, each 256-byte aligned). */
 size_t omni_try_int8_gemm_workspace_size(int64_t rows, int64_t width);
 
+/* Workspace bytes with which omni_try_int8_gemm and omni_convrot_linear also
+ * split K for this shape (omni_try_int8_gemm_workspace_size(rows, width)
+ * plus omni_w8a8_gemm_workspace_size(rows, columns, width)): the reference's
+ * own 256-row shapes run in a fraction of the unsplit time. No counterpart
+ * in the reference, whose try_int8_gemm allocates per call
+ * (int8_matmul.rs:386-471). The workspace needs no initialisation; outputs
+ * are bit-identical to the unsplit call. */
+size_t omni_try_int8_gemm_split_workspace_size(int64_t rows, int64_t columns, int64_t width);
+
 /* The whole reference operator, x @ W^T after per-row int8 quantisation of x.
  * Replaces try_int8_gemm, crates/omni-kernel/src/int8_matmul.rs:505-560
  * (and its launch :386-471). Shape guard as :517-521: columns = scale_len;
  * returns OMNI_NOT_HANDLED (the reference's None) unless width % 4 == 0,
  * w_packed_len == columns * width / 4 and zero_len == columns.
- * x [rows][width] (x_dtype f32 or f16, contiguous) -> out f32 [rows][columns]. */
+ * x [rows][width] (x_dtype f32 or f16, contiguous) -> out f32 [rows][columns].
+ * workspace: at least omni_try_int8_gemm_workspace_size(rows, width) bytes,
+ * 256-byte aligned; with omni_try_int8_gemm_split_workspace_size(rows,
+ * columns, width) bytes the GEMM may split K (same results; one more
+ * launch, the reduction of the partial sums). */
 int omni_try_int8_gemm(const void* x, int x_dtype, int64_t rows, int64_t width,
                        const int32_t* w_packed, int64_t w_packed_len, const float* w_scale,
                        int64_t scale_len, const int32_t* w_zero, int64_t zero_len, float* out,
@@ -147,7 +163,9 @@ int omni_try_int8_gemm(const void* x, int x_dtype, int64_t rows, int64_t width,
  * in a static device array of OMNI_NOALLOC_SCRATCH_BYTES that each GPU the
  * library runs on holds until the process ends; shapes whose
  * omni_try_int8_gemm_workspace_size(rows, width) exceeds it are rejected
- * with OMNI_BAD_ARGUMENT (64 MiB covers 4352 x 12288 activations). The call
+ * with OMNI_BAD_ARGUMENT (64 MiB covers 4352 x 12288 activations); where
+ * omni_try_int8_gemm_split_workspace_size fits, the GEMM splits K as
+ * omni_try_int8_gemm does with that workspace. The call
  * allocates nothing. Every call on one GPU shares that GPU's array: calls
  * that overlap in time on one GPU (other streams, other host threads) race
  * on it and must be serialised by the caller. Arguments, guard, result and
@@ -184,8 +202,9 @@ int omni_convrot_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t
  * (columns = scale_len) plus width % 256 == 0; OMNI_NOT_HANDLED where the
  * reference panics. out_dtype OMNI_F16 (the model's Precision::F16: the f32
  * result rounded once to nearest even, convrot.rs:91) or OMNI_F32.
- * x contiguous [rows][width]; workspace as omni_try_int8_gemm
- * (omni_try_int8_gemm_workspace_size(rows, width) bytes, 256-byte aligned). */
+ * x contiguous [rows][width]; workspace as omni_try_int8_gemm (at least
+ * omni_try_int8_gemm_workspace_size(rows, width) bytes, 256-byte aligned;
+ * with omni_try_int8_gemm_split_workspace_size bytes the GEMM may split K). */
 int omni_convrot_linear(const void* x, int x_dtype, int64_t rows, int64_t width,
                         const int32_t* w_packed, int64_t w_packed_len, const float* w_scale,
                         int64_t scale_len, const int32_t* w_zero, int64_t zero_len, void* out,

@@ -112,7 +112,9 @@ inline std::optional<DeviceTensor> try_int8_gemm(const DeviceTensor& x, const De
         w_scale.dtype != DType::F32 || w_zero.dtype != DType::I32)
         throw Int8Error(OMNI_BAD_ARGUMENT, "try_int8_gemm: x f32/f16, w_packed i32, w_scale f32, w_zero i32");
     DeviceTensor out{alloc.allocate((size_t)(rows * columns) * 4, stream), {rows, columns}, DType::F32};
-    const size_t ws_bytes = omni_try_int8_gemm_workspace_size(rows, width);
+    // Room for the split-K partial sums too: the reference's 256-row shapes
+    // split K.
+    const size_t ws_bytes = omni_try_int8_gemm_split_workspace_size(rows, columns, width);
     void* ws = alloc.allocate(ws_bytes, stream);
     const int st = omni_try_int8_gemm(x.data, x.dtype == DType::F16 ? OMNI_F16 : OMNI_F32, rows,
                                       width, static_cast<const int32_t*>(w_packed.data),

@@ -121,11 +121,25 @@ int w4a16_kind(int64_t rows, int64_t columns, int64_t width) {
 
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// A split-K GEMM workspace: int32 partial sums (none: no split).
+struct SplitWorkspace {
+    int32_t* partial = nullptr;
+    int64_t partial_elems = 0;
+};
+
+SplitWorkspace split_workspace(void* workspace, size_t bytes) {
+    SplitWorkspace w;
+    if (!workspace) return w;
+    w.partial = static_cast<int32_t*>(workspace);
+    w.partial_elems = (int64_t)(bytes / sizeof(int32_t));
+    return w;
+}
+
 int run_w8a8(const int32_t* x_packed, const float* x_scale, const int32_t* x_sum,
              const int32_t* w_packed, const float* w_scale, const int32_t* w_zero,
              const float* bias, int64_t rows, int64_t columns, int64_t width, void* out,
              int out_dtype, int32_t* acc_dump, int lowering, hipStream_t stream,
-             int32_t* partial = nullptr, int64_t partial_elems = 0) {
+             SplitWorkspace split = SplitWorkspace()) {
     omni::W8A8Args a;
     a.x = reinterpret_cast<const uint8_t*>(x_packed);
     a.x_scale = x_scale;
@@ -140,8 +154,8 @@ int run_w8a8(const int32_t* x_packed, const float* x_scale, const int32_t* x_sum
     a.columns = columns;
     a.width = width;
     a.out_f16 = out_dtype == OMNI_F16;
-    a.partial = partial;
-    a.partial_elems = partial_elems;
+    a.partial = split.partial;
+    a.partial_elems = split.partial_elems;
     int chosen = lowering == OMNI_LOWERING_AUTO ? omni_w8a8_lowering(width) : lowering;
     // The MFMA kernels need 16-byte rows and keep in-tile output offsets in
     // 32 bits (in bytes: 256 * columns * 4 < 2^32).
@@ -248,7 +262,19 @@ int try_int8_gemm_checks(const char* name, const void* x, int x_dtype, int64_t r
 
 int try_int8_gemm_run(const void* x, int x_dtype, int64_t rows, int64_t width,
                       const int32_t* w_packed, const float* w_scale, int64_t columns,
-                      const int32_t* w_zero, float* out, uint8_t* ws, void* stream);
+                      const int32_t* w_zero, float* out, uint8_t* ws, size_t ws_bytes, void* stream);
+
+int w8a8_gemm_checked(const int32_t* x_packed, const float* x_scale, const int32_t* x_sum,
+                      const int32_t* w_packed, const float* w_scale, const int32_t* w_zero,
+                      const float* bias, int64_t rows, int64_t columns, int64_t width, void* out,
+                      int out_dtype, int32_t* acc_dump, int lowering, SplitWorkspace split, void* stream);
+
+// The activation block of the operator workspaces: codes, row scales, row
+// sums, each 256-byte aligned; a split-K GEMM workspace follows it.
+size_t activation_bytes(int64_t rows, int64_t width) {
+    return round_up((size_t)rows * (size_t)width, 256) + round_up((size_t)rows * 4, 256) +
+           round_up((size_t)rows * 4, 256);
+}
 
 }  // namespace
 
@@ -306,6 +332,21 @@ int omni_w8a8_gemm_ws(const int32_t* x_packed, const float* x_scale, const int32
                       size_t workspace_bytes, void* stream) {
     if (workspace_bytes > 0 && (!workspace || !aligned(workspace, 256)))
         return fail(OMNI_BAD_ARGUMENT, "w8a8_gemm: workspace must be 256-byte aligned");
+    return w8a8_gemm_checked(x_packed, x_scale, x_sum, w_packed, w_scale, w_zero, bias, rows, columns, width,
+                             out, out_dtype, acc_dump, lowering, split_workspace(workspace, workspace_bytes),
+                             stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+// omni_w8a8_gemm_ws after its workspace check (shared with the operators,
+// which carve the split-K workspace out of their own).
+int w8a8_gemm_checked(const int32_t* x_packed, const float* x_scale, const int32_t* x_sum,
+                      const int32_t* w_packed, const float* w_scale, const int32_t* w_zero,
+                      const float* bias, int64_t rows, int64_t columns, int64_t width, void* out,
+                      int out_dtype, int32_t* acc_dump, int lowering, SplitWorkspace split, void* stream) {
     if (rows < 0 || columns < 0 || width < 0)
         return fail(OMNI_BAD_ARGUMENT, "w8a8_gemm: negative size");
     if (out_dtype != OMNI_F32 && out_dtype != OMNI_F16)
@@ -324,14 +365,21 @@ int omni_w8a8_gemm_ws(const int32_t* x_packed, const float* x_scale, const int32
     int st = check_current_device();
     if (st != OMNI_OK) return st;
     return run_w8a8(x_packed, x_scale, x_sum, w_packed, w_scale, w_zero, bias, rows, columns,
-                    width, out, out_dtype, acc_dump, lowering, static_cast<hipStream_t>(stream),
-                    static_cast<int32_t*>(workspace), (int64_t)(workspace_bytes / sizeof(int32_t)));
+                    width, out, out_dtype, acc_dump, lowering, static_cast<hipStream_t>(stream), split);
 }
+
+}  // namespace
+
+extern "C" {
 
 size_t omni_try_int8_gemm_workspace_size(int64_t rows, int64_t width) {
     if (rows < 0 || width < 0) return 0;
-    return round_up((size_t)rows * (size_t)width, 256) + round_up((size_t)rows * 4, 256) +
-           round_up((size_t)rows * 4, 256);
+    return activation_bytes(rows, width);
+}
+
+size_t omni_try_int8_gemm_split_workspace_size(int64_t rows, int64_t columns, int64_t width) {
+    if (rows < 0 || width < 0 || columns < 0) return 0;
+    return activation_bytes(rows, width) + omni_w8a8_gemm_workspace_size(rows, columns, width);
 }
 
 int omni_try_int8_gemm(const void* x, int x_dtype, int64_t rows, int64_t width,
@@ -347,7 +395,7 @@ int omni_try_int8_gemm(const void* x, int x_dtype, int64_t rows, int64_t width,
     if (!workspace) return fail(OMNI_BAD_ARGUMENT, "try_int8_gemm: null pointer");
     if (!aligned(workspace, 256)) return fail(OMNI_BAD_ARGUMENT, "try_int8_gemm: workspace must be 256-byte aligned");
     return try_int8_gemm_run(x, x_dtype, rows, width, w_packed, w_scale, scale_len, w_zero, out,
-                             static_cast<uint8_t*>(workspace), stream);
+                             static_cast<uint8_t*>(workspace), workspace_bytes, stream);
 }
 
 int omni_try_int8_gemm_noalloc(const void* x, int x_dtype, int64_t rows, int64_t width,
@@ -369,7 +417,7 @@ int omni_try_int8_gemm_noalloc(const void* x, int x_dtype, int64_t rows, int64_t
     st = scratch_of_current_device(&ws);
     if (st != OMNI_OK) return st;
     return try_int8_gemm_run(x, x_dtype, rows, width, w_packed, w_scale, scale_len, w_zero, out,
-                             ws, stream);
+                             ws, kScratchBytes, stream);
 }
 
 int omni_convrot_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t width,
@@ -435,13 +483,15 @@ int omni_convrot_linear(const void* x, int x_dtype, int64_t rows, int64_t width,
     float* x_scale = reinterpret_cast<float*>(ws + round_up((size_t)rows * width, 256));
     int32_t* x_sum = reinterpret_cast<int32_t*>(ws + round_up((size_t)rows * width, 256) +
                                                 round_up((size_t)rows * 4, 256));
-    int st = omni_convrot_quantize_rows(x, x_dtype, rows, width, width, 256, x_packed, x_scale,
-                                        x_sum, stream);
+    // Beyond the activation block: the split-K partial sums.
+    const size_t act = activation_bytes(rows, width);
+    const SplitWorkspace split = split_workspace(ws + act, workspace_bytes - act);
+    int st = omni_convrot_quantize_rows(x, x_dtype, rows, width, width, 256, x_packed, x_scale, x_sum, stream);
     if (st != OMNI_OK) return st;
     // The reference casts the f32 result to the model precision after the op
     // (convrot.rs:91); the GEMM's f16 epilogue applies that same one rounding.
-    return omni_w8a8_gemm(x_packed, x_scale, x_sum, w_packed, w_scale, w_zero, nullptr, rows,
-                          columns, width, out, out_dtype, nullptr, OMNI_LOWERING_AUTO, stream);
+    return w8a8_gemm_checked(x_packed, x_scale, x_sum, w_packed, w_scale, w_zero, nullptr, rows, columns,
+                             width, out, out_dtype, nullptr, OMNI_LOWERING_AUTO, split, stream);
 }
 
 size_t omni_w8a16_gemm_workspace_size(int64_t rows, int64_t columns, int64_t width) {
@@ -578,19 +628,21 @@ int omni_f16_gemm(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t co
 namespace {
 
 // Quantise x into the workspace (codes, then row scales, then row sums, each
-// 256-byte aligned), then the GEMM with the reference's f32 epilogue.
+// 256-byte aligned), then the GEMM with the reference's f32 epilogue. What
+// the workspace holds beyond that block is the GEMM's split-K partial sums.
 int try_int8_gemm_run(const void* x, int x_dtype, int64_t rows, int64_t width,
                       const int32_t* w_packed, const float* w_scale, int64_t columns,
-                      const int32_t* w_zero, float* out, uint8_t* ws, void* stream) {
+                      const int32_t* w_zero, float* out, uint8_t* ws, size_t ws_bytes, void* stream) {
     int32_t* x_packed = reinterpret_cast<int32_t*>(ws);
     float* x_scale = reinterpret_cast<float*>(ws + round_up((size_t)rows * width, 256));
     int32_t* x_sum = reinterpret_cast<int32_t*>(ws + round_up((size_t)rows * width, 256) +
                                                 round_up((size_t)rows * 4, 256));
-    int st = omni_int8_quantize_rows(x, x_dtype, rows, width, width, x_packed, x_scale, x_sum,
-                                     stream);
+    const size_t act = activation_bytes(rows, width);
+    const SplitWorkspace split = split_workspace(ws + act, ws_bytes - act);
+    int st = omni_int8_quantize_rows(x, x_dtype, rows, width, width, x_packed, x_scale, x_sum, stream);
     if (st != OMNI_OK) return st;
-    return omni_w8a8_gemm(x_packed, x_scale, x_sum, w_packed, w_scale, w_zero, nullptr, rows,
-                          columns, width, out, OMNI_F32, nullptr, OMNI_LOWERING_AUTO, stream);
+    return w8a8_gemm_checked(x_packed, x_scale, x_sum, w_packed, w_scale, w_zero, nullptr, rows, columns,
+                             width, out, OMNI_F32, nullptr, OMNI_LOWERING_AUTO, split, stream);
 }
 
 }  // namespace

@@ -181,7 +181,9 @@ def try_int8_gemm(x: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor
     w_scale = w_scale.to(torch.float32).contiguous()
     w_zero = w_zero.to(torch.int32).contiguous()
     L = _lib.lib()
-    ws_bytes = L.omni_try_int8_gemm_workspace_size(rows, width)
+    # With room for the split-K partial sums the GEMM splits K where that
+    # pays.
+    ws_bytes = L.omni_try_int8_gemm_split_workspace_size(rows, columns, width)
     workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
     out = torch.empty((rows, columns), dtype=torch.float32, device=device)
     st = _lib.check(L.omni_try_int8_gemm(

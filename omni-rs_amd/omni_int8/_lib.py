@@ -39,6 +39,7 @@ SIGNATURES = {
     "omni_w8a8_gemm_ws": (_INT, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _INT, _P, _INT, _P,
                                  ctypes.c_size_t, _P]),
     "omni_try_int8_gemm_workspace_size": (ctypes.c_size_t, [_I64, _I64]),
+    "omni_try_int8_gemm_split_workspace_size": (ctypes.c_size_t, [_I64, _I64, _I64]),
     "omni_try_int8_gemm": (_INT, [_P, _INT, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _P,
                                   ctypes.c_size_t, _P]),
     "omni_try_int8_gemm_noalloc": (_INT, [_P, _INT, _I64, _I64, _P, _I64, _P, _I64, _P, _I64,

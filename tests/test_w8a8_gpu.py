@@ -429,6 +429,54 @@ def test_north_star_try_int8_gemm_as_benched(oracle, width, columns):
     assert np.array_equal(host(out)[idx].view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("columns,width", [(4096, 4096), (12288, 4096), (4096, 12288)])
+def test_try_int8_gemm_split_k_reference_shapes(oracle, columns, width):
+    # The reference's own 256-row int8 GEMM benchmark shapes
+    # (docs/qwen-image-convrot-optimization-research.md:5) through the
+    # operator. With omni_try_int8_gemm_split_workspace_size bytes the GEMM
+    # splits K where that pays (256 x 4096 from K = 4096 on; 256 x 12288 has
+    # 96 tiles and does not split), with a workspace handed over full of
+    # garbage: every output bit equal to the unsplit operator's (the plain
+    # workspace), to a second call on the same workspace, to the no-alloc
+    # entry (whose static scratch holds the split too), and to the C oracle
+    # on sampled rows, with zero points.
+    from omni_int8 import _lib
+    L = _lib.lib()
+    rows = 256
+    rng = np.random.default_rng(columns + 7 * width)
+    x = rng.standard_normal((rows, width)).astype(np.float16)
+    w = rng.integers(-127, 128, (columns, width), dtype=np.int8)
+    scale = rng.uniform(0.002, 0.02, columns).astype(np.float32)
+    zero = rng.integers(-3, 4, columns).astype(np.int32)
+    xd, wp, sd, zd = dev(x), dev(w).view(torch.int32).reshape(-1), dev(scale), dev(zero)
+    plain_bytes = L.omni_try_int8_gemm_workspace_size(rows, width)
+    split_bytes = L.omni_try_int8_gemm_split_workspace_size(rows, columns, width)
+    assert (split_bytes > plain_bytes) == (columns == 4096), (plain_bytes, split_bytes)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def call(ws, nbytes):
+        out = torch.empty((rows, columns), dtype=torch.float32, device="cuda")
+        st = L.omni_try_int8_gemm(xd.data_ptr(), oi.OMNI_F16, rows, width, wp.data_ptr(), wp.numel(),
+                                  sd.data_ptr(), columns, zd.data_ptr(), columns, out.data_ptr(),
+                                  ws.data_ptr(), nbytes, stream)
+        assert st == 0, _lib.last_error()
+        return out
+
+    plain = call(torch.empty(plain_bytes, dtype=torch.uint8, device="cuda"), plain_bytes)
+    ws = torch.full((split_bytes,), 0x5A, dtype=torch.uint8, device="cuda")
+    split = call(ws, split_bytes)
+    again = call(ws, split_bytes)
+    noalloc = torch.empty((rows, columns), dtype=torch.float32, device="cuda")
+    st = L.omni_try_int8_gemm_noalloc(xd.data_ptr(), oi.OMNI_F16, rows, width, wp.data_ptr(), wp.numel(),
+                                      sd.data_ptr(), columns, zd.data_ptr(), columns, noalloc.data_ptr(), stream)
+    assert st == 0, _lib.last_error()
+    for got in (split, again, noalloc, oi.try_int8_gemm(xd, wp, sd, zd)):
+        assert torch.equal(got.view(torch.int32), plain.view(torch.int32))
+    idx = np.array([0, 1, 77, 128, 200, rows - 1])
+    want = oracle.int8_gemm(x[idx].astype(np.float32), w, scale, zero)
+    assert np.array_equal(host(split)[idx].view(np.uint32), want.view(np.uint32))
+
+
 @pytest.mark.parametrize("rows,width,columns", [(1, 64, 7), (300, 512, 513), (700, 3072, 650),
                                                 (1000, 4096, 1500)])
 @pytest.mark.parametrize("lowering", [oi.OMNI_LOWERING_MFMA, oi.OMNI_LOWERING_SCALAR])
@@ -561,15 +609,16 @@ def test_w8a8_split_k_workspace_contract(monkeypatch):
     zero = dev(rng.integers(-3, 4, columns).astype(np.int32))
     ref = oi.w8a8_gemm(codes, rs, total, w, scale, zero)
     stream = torch.cuda.current_stream().cuda_stream
-    for ints in (4 * rows * columns, 2 * rows * columns + 3, 0):
-        ws = torch.empty(max(ints, 1) * 4, dtype=torch.uint8, device="cuda")
-        out = torch.empty((rows, columns), dtype=torch.float32, device="cuda")
-        st = L.omni_w8a8_gemm_ws(codes.data_ptr(), rs.data_ptr(), total.data_ptr(), w.data_ptr(),
-                                 scale.data_ptr(), zero.data_ptr(), None, rows, columns, width, out.data_ptr(),
-                                 oi.OMNI_F32, None, oi.OMNI_LOWERING_AUTO, ws.data_ptr() if ints else None,
-                                 ints * 4, stream)
-        assert st == 0, _lib.last_error()
-        assert torch.equal(out.view(torch.int32), ref.view(torch.int32)), ints
+    for nbytes in (4 * rows * columns * 4, (2 * rows * columns + 3) * 4, 0):
+        ws = torch.full((max(nbytes, 1),), 0x5A, dtype=torch.uint8, device="cuda")
+        for call in range(2):  # the same workspace again: it needs no initialisation
+            out = torch.empty((rows, columns), dtype=torch.float32, device="cuda")
+            st = L.omni_w8a8_gemm_ws(codes.data_ptr(), rs.data_ptr(), total.data_ptr(), w.data_ptr(),
+                                     scale.data_ptr(), zero.data_ptr(), None, rows, columns, width,
+                                     out.data_ptr(), oi.OMNI_F32, None, oi.OMNI_LOWERING_AUTO,
+                                     ws.data_ptr() if nbytes else None, nbytes, stream)
+            assert st == 0, _lib.last_error()
+            assert torch.equal(out.view(torch.int32), ref.view(torch.int32)), (nbytes, call)
     bad = torch.empty(1024, dtype=torch.uint8, device="cuda")
     st = L.omni_w8a8_gemm_ws(codes.data_ptr(), rs.data_ptr(), total.data_ptr(), w.data_ptr(), scale.data_ptr(),
                              zero.data_ptr(), None, rows, columns, width, out.data_ptr(), oi.OMNI_F32, None,
