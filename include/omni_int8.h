@@ -76,6 +76,17 @@ int omni_w8a8_lowering(int64_t width);
 /* Message for the last non-OK status returned on this thread. */
 const char* omni_int8_last_error(void);
 
+/* Tuning and test knobs: the OMNI_W8A8_TILE / _SPLITS, OMNI_W8A16_* ,
+ * OMNI_W4A16_* and OMNI_F16_* variables that pin a kernel variant or a
+ * split count. The library reads them from the environment once per
+ * process, not on every launch; this call overrides one for the rest of the
+ * process (thread-safe): mode 2 = `value`, mode 1 = unset (the shape rules
+ * decide), mode 0 = back to the environment's value. No counterpart in the
+ * reference (its one switch, OMNI_CONVROT_TENSOROPS, int8_tensorops.rs:15-20,
+ * is still read on every call, as there). OMNI_BAD_ARGUMENT for an unknown
+ * name. */
+int omni_int8_set_tuning(const char* name, int mode, int value);
+
 /* Per-row dynamic symmetric int8 quantisation.
  * Replaces quantize_rows + quantize_i8, crates/omni-kernel/src/int8_matmul.rs:23-118
  * (host twin: crates/omni-kernel/src/int8_host.rs:31-39):

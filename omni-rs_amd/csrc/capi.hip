@@ -6,6 +6,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <atomic>
 #include <mutex>
 
 #include "../../include/omni_int8.h"
@@ -75,13 +76,39 @@ bool force_scalar() {
 
 bool aligned(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
 
-// OMNI_W8A16_ROUTE=1 keeps 5..64-row W8A16 and W4A16 calls on the skinny
-// kernel, =2 sends them to the tiled MFMA GEMM (test aids; read on every
-// call); unset, the measured rule below.
-int w8a16_route() {
-    const char* v = std::getenv("OMNI_W8A16_ROUTE");
-    return v ? std::atoi(v) : 0;
+// Tuning knobs (omni::knob): the environment as read once per process, and
+// tests' overrides (omni_int8_set_tuning). An override state is 0 (none:
+// the environment's value applies), 1 (the knob reads as unset) or 2 (it
+// reads as the override value).
+constexpr int kKnobs = (int)omni::Knob::Count;
+constexpr const char* kKnobNames[kKnobs] = {
+    "OMNI_W8A8_TILE",   "OMNI_W8A8_SPLITS",      "OMNI_W8A16_GEMV",  "OMNI_F16_GEMV",
+    "OMNI_W8A16_SKINNY", "OMNI_W8A16_SKINNY_SPLIT", "OMNI_W8A16_TILE", "OMNI_W8A16_SPLITS",
+    "OMNI_W8A16_ROUTE", "OMNI_W4A16_GEMV",       "OMNI_W4A16_SKINNY_SPLIT", "OMNI_W4A16_SPLITS",
+    "OMNI_W4A16_TILE",  "OMNI_F16_TILE"};
+std::once_flag g_knob_once;
+bool g_knob_env_set[kKnobs];
+int g_knob_env[kKnobs];
+std::atomic<int> g_knob_state[kKnobs];
+std::atomic<int> g_knob_value[kKnobs];
+
+void read_knob_environment() {
+    std::call_once(g_knob_once, [] {
+        for (int i = 0; i < kKnobs; ++i) {
+            const char* v = std::getenv(kKnobNames[i]);
+            g_knob_env_set[i] = v != nullptr;
+            g_knob_env[i] = v ? std::atoi(v) : 0;
+        }
+    });
 }
+
+// Compute units per device, cached (0: not yet asked).
+std::atomic<int> g_cus[kMaxDevices];
+
+// OMNI_W8A16_ROUTE=1 keeps 5..64-row W8A16 and W4A16 calls on the skinny
+// kernel, =2 sends them to the tiled MFMA GEMM (test aids, a tuning knob);
+// unset, the measured rule below.
+int w8a16_route() { return omni::knob(omni::Knob::W8A16Route, 0); }
 
 // 17..64 rows: the skinny kernel streams the weights once per 16 rows, the
 // GEMM once per 64 to 256, so the GEMM wins on big matrices (MI355X, W8A16
@@ -278,7 +305,51 @@ size_t activation_bytes(int64_t rows, int64_t width) {
 
 }  // namespace
 
+namespace omni {
+
+int knob(Knob k, int unset) {
+    read_knob_environment();
+    const int i = (int)k;
+    if (i < 0 || i >= kKnobs) return unset;
+    switch (g_knob_state[i].load(std::memory_order_acquire)) {
+        case 1: return unset;
+        case 2: return g_knob_value[i].load(std::memory_order_relaxed);
+        default: return g_knob_env_set[i] ? g_knob_env[i] : unset;
+    }
+}
+
+int num_cus() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    int n = g_cus[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        n = 256;
+    }
+    g_cus[dev].store(n, std::memory_order_relaxed);  // every thread stores the same value
+    return n;
+}
+
+}  // namespace omni
+
 extern "C" {
+
+int omni_int8_set_tuning(const char* name, int mode, int value) {
+    if (!name) return fail(OMNI_BAD_ARGUMENT, "set_tuning: null name");
+    if (mode < 0 || mode > 2) return fail(OMNI_BAD_ARGUMENT, "set_tuning: mode %d", mode);
+    read_knob_environment();
+    for (int i = 0; i < kKnobs; ++i) {
+        if (std::strcmp(name, kKnobNames[i]) != 0) continue;
+        g_knob_value[i].store(value, std::memory_order_relaxed);
+        g_knob_state[i].store(mode, std::memory_order_release);
+        return OMNI_OK;
+    }
+    return fail(OMNI_BAD_ARGUMENT, "set_tuning: unknown knob %s", name);
+}
 
 int omni_int8_arch_supported(int device) { return probe_arch(device); }
 

@@ -6,6 +6,32 @@
 
 namespace omni {
 
+// Tuning and test knobs (kernel pins, split overrides). Each one's value is a
+// test's override when one is set (omni_int8_set_tuning), else the
+// environment variable of the knob's name as read once per process, else
+// `unset`; reading one on a launch is two atomic loads, no getenv.
+enum class Knob : int {
+    W8A8Tile,          // OMNI_W8A8_TILE
+    W8A8Splits,        // OMNI_W8A8_SPLITS
+    W8A16Gemv,         // OMNI_W8A16_GEMV
+    F16Gemv,           // OMNI_F16_GEMV
+    W8A16Skinny,       // OMNI_W8A16_SKINNY
+    W8A16SkinnySplit,  // OMNI_W8A16_SKINNY_SPLIT
+    W8A16Tile,         // OMNI_W8A16_TILE
+    W8A16Splits,       // OMNI_W8A16_SPLITS
+    W8A16Route,        // OMNI_W8A16_ROUTE
+    W4A16Gemv,         // OMNI_W4A16_GEMV
+    W4A16SkinnySplit,  // OMNI_W4A16_SKINNY_SPLIT
+    W4A16Splits,       // OMNI_W4A16_SPLITS
+    W4A16Tile,         // OMNI_W4A16_TILE
+    F16Tile,           // OMNI_F16_TILE
+    Count
+};
+int knob(Knob k, int unset);
+
+// Compute units of the current device (cached per device, thread-safe).
+int num_cus();
+
 hipError_t launch_quantize_rows(const void* x, bool x_is_f16, int64_t rows, int64_t width,
                                 int64_t ld, uint8_t* codes, float* scale, int32_t* sum,
                                 hipStream_t stream);

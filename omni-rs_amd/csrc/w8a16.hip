@@ -330,12 +330,8 @@ __global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
 
 // OMNI_W8A16_GEMV=<cpl><r> (e.g. 14 = one chunk per lane, four rows per
 // workgroup) pins the int8 GEMV configuration, OMNI_F16_GEMV the f16 one
-// (tuning aids; unset = heuristic). Read on every launch so one process can
-// time each configuration.
-int gemv_cfg_override(int wb) {
-    const char* v = std::getenv(wb == 8 ? "OMNI_W8A16_GEMV" : "OMNI_F16_GEMV");
-    return v ? std::atoi(v) : 0;
-}
+// (tuning knobs, omni::knob; unset = heuristic).
+int gemv_cfg_override(int wb) { return knob(wb == 8 ? Knob::W8A16Gemv : Knob::F16Gemv, 0); }
 
 template <int MR, int CPL, int R, int WB, int B = 1, int KF = 0>
 hipError_t launch_gemv_cfg(const W8A16Args& a, hipStream_t stream) {
@@ -771,11 +767,10 @@ int cu_count();
 // 4096, one round) 9.6 against 7.8, and 8 x 3584 -> 4608 12.3 against 10.6:
 // one round is bound by the cold fetch of x and the first weight latency, not
 // by the x traffic the split saves, and the reduction launch adds ~1.5 us.
-// OMNI_W8A16_SKINNY_SPLIT=<n> pins n (0: off; test aid, read on every call).
+// OMNI_W8A16_SKINNY_SPLIT=<n> pins n (0: off; test aid, a tuning knob).
 int skinny_splits(int64_t rows, int64_t width, int64_t columns, int64_t partial_elems, int cus) {
     if (rows > 16 || width % 64 != 0) return 1;
-    const char* v = std::getenv("OMNI_W8A16_SKINNY_SPLIT");
-    int want = v ? std::atoi(v) : -1;
+    int want = knob(Knob::W8A16SkinnySplit, -1);
     if (want == 0) return 1;
     if (want < 0) {
         if (width > kSkinnyLdsMaxK || columns < 32LL * cus) return 1;
@@ -789,11 +784,8 @@ int skinny_splits(int64_t rows, int64_t width, int64_t columns, int64_t partial_
 }
 
 // OMNI_W8A16_SKINNY=1 keeps 5..16-row calls on w8a16_skinny_kernel instead
-// of the LDS-staged kernel (test aid; read on every call).
-int skinny_route() {
-    const char* v = std::getenv("OMNI_W8A16_SKINNY");
-    return v ? std::atoi(v) : 0;
-}
+// of the LDS-staged kernel (test aid; a tuning knob).
+int skinny_route() { return knob(Knob::W8A16Skinny, 0); }
 
 template <int MB, int WB>
 hipError_t launch_skinny_cfg(const W8A16Args& a, hipStream_t stream) {
@@ -1763,13 +1755,7 @@ hipError_t launch_skinny_split(const W8A16Args& a, int splits, hipStream_t strea
     return hipGetLastError();
 }
 
-int cu_count() {
-    int dev = 0, cus = 256;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        cus = 256;
-    return cus;
-}
+int cu_count() { return num_cus(); }
 
 // Largest split count <= want that leaves every split of ktiles K tiles
 // non-empty and whose partial sums fit in a.partial_elems floats.
@@ -1845,11 +1831,8 @@ hipError_t launch_w8a16_skinny(const W8A16Args& a, hipStream_t stream) { return 
 // 256 x 256 (waves 64 x 128) / 256 x 256 (waves 128 x 64) with eight waves
 // (rings: K % 64 == 0 only). OMNI_W8A16_SPLITS=<n>
 // adds n-way split K to a pinned ring (or to the shape rule's choice) when
-// the call brings a workspace. Both are read on every call.
-int w8a16_tile_override() {
-    const char* v = std::getenv("OMNI_W8A16_TILE");
-    return v ? std::atoi(v) : 0;
-}
+// the call brings a workspace. Both are tuning knobs (omni::knob).
+int w8a16_tile_override() { return knob(Knob::W8A16Tile, 0); }
 
 // The kernel and split count launch_w8a16_mfma runs for a shape: cfg as
 // OMNI_W8A16_TILE numbers them (0: the register-staged kernels), splits > 1
@@ -1862,8 +1845,7 @@ struct W16Plan {
 // ws_limited: split only as far as a.partial holds (a launch); else assume
 // the workspace the plan asks for (the size query).
 W16Plan plan_w8a16(const W8A16Args& a, int cus, bool ws_limited) {
-    const char* sv = std::getenv("OMNI_W8A16_SPLITS");
-    const int split_override = sv ? std::atoi(sv) : 0;
+    const int split_override = knob(Knob::W8A16Splits, 0);
     const bool ring_ok = ring16_fits(a);
     const int ov = w8a16_tile_override();
     if (ov == 1 || ov == 2 || (ov >= 4 && ov <= 12 && ring_ok) || (ov >= 16 && ov <= 18 && ring_ok))
@@ -1979,8 +1961,7 @@ hipError_t launch_w4a16_gemv(const W8A16Args& a, hipStream_t stream) {
     if (T > 1024) return hipErrorInvalidValue;  // the caller keeps width <= 32768
     // OMNI_W4A16_GEMV=<r><b> pins r rows per batch and b batches per
     // workgroup (tuning aid); unset: the measured choice below.
-    const char* ov = std::getenv("OMNI_W4A16_GEMV");
-    int cfg = ov ? std::atoi(ov) : 0;
+    int cfg = knob(Knob::W4A16Gemv, 0);
     // Measured on MI355X: 4 rows per workgroup from 4 MB of codes (7.6 us
     // at 4096 x 14336), two batches of 4 from 64 MB (43 us at the 128256-row
     // vocabulary head), 2 rows below 4 MB. With 2-4 activation rows, 8 rows
@@ -2034,12 +2015,11 @@ hipError_t launch_w4a16_gemv(const W8A16Args& a, hipStream_t stream) {
 // workgroups: MI355X, 16 x 4096 -> 14336 25.2 us split four ways against
 // 31.1, the 128256-row head 153 against 226, 16 x 3584 -> 18944 27.1
 // against 28.2 (8 rows: 25.2 against 23.9); 8 x 2048 -> 8192 10.1 split
-// two ways against 8.5. OMNI_W4A16_SKINNY_SPLIT=<n> pins n (0: off; test aid, read
-// on every call).
+// two ways against 8.5. OMNI_W4A16_SKINNY_SPLIT=<n> pins n (0: off; test aid, a
+// tuning knob).
 int w4_skinny_splits(int64_t rows, int64_t width, int64_t columns, int64_t partial_elems, int cus) {
     if (rows > 16 || width % 64 != 0 || width >= (int64_t(1) << 31)) return 1;
-    const char* v = std::getenv("OMNI_W4A16_SKINNY_SPLIT");
-    int want = v ? std::atoi(v) : -1;
+    int want = knob(Knob::W4A16SkinnySplit, -1);
     if (want == 0) return 1;
     if (want < 0) {
         if (columns < 32LL * cus || width < 3072 || width > 4 * kSkinnySplitMaxKS) return 1;
@@ -2076,7 +2056,7 @@ hipError_t launch_w4a16_skinny(const W8A16Args& a, hipStream_t stream) {
 // (waves 64 x 128) / 256 x 256 (waves 128 x 64) (rings: K % 64 == 0, group
 // % 64 == 0, K / group even, scales 4-byte aligned); OMNI_W4A16_SPLITS=<n>
 // adds n-way split K to a pinned ring when the call brings a workspace.
-// Both are read on every call.
+// Both are tuning knobs (omni::knob).
 struct W4Plan {
     int cfg;     // tile id as above
     int splits;  // K splits (> 1 needs a workspace)
@@ -2090,10 +2070,8 @@ bool w4_ring_ok(const W8A16Args& a) {
 }
 
 W4Plan plan_w4a16(const W8A16Args& a, int cus, bool ws_limited) {
-    const char* sv = std::getenv("OMNI_W4A16_SPLITS");
-    const int split_override = sv ? std::atoi(sv) : 0;
-    const char* ov = std::getenv("OMNI_W4A16_TILE");
-    const int t = ov ? std::atoi(ov) : 0;
+    const int split_override = knob(Knob::W4A16Splits, 0);
+    const int t = knob(Knob::W4A16Tile, 0);
     const bool ring_ok = w4_ring_ok(a);
     if (t == 1 || t == 2) return {t, 1};
     if (ring_ok && (t == 4 || t == 5 || t == 6 || t == 10 || (t >= 16 && t <= 18)))
@@ -2188,12 +2166,11 @@ hipError_t launch_f16_skinny(const W8A16Args& a, hipStream_t stream) { return la
 // 128 x 256, 7/8 = ring 256 x 256 / 256 x 128 on 32-element K tiles, 10 =
 // eight-wave ring 256 x 128, 12 / 13 = eight-wave ring 256 x 256 on 32- /
 // 64-element K tiles, 14 = the latter with waves 128 x 64 instead of 64 x 128
-// (rings: K % 64 == 0 only). Read on every call.
+// (rings: K % 64 == 0 only). A tuning knob (omni::knob).
 hipError_t launch_f16_mfma(const W8A16Args& a, hipStream_t stream) {
     if (a.rows == 0 || a.columns == 0) return hipSuccess;
     const bool ring_ok = ring16_fits(a);
-    const char* ov = std::getenv("OMNI_F16_TILE");
-    switch (ov ? std::atoi(ov) : 0) {
+    switch (knob(Knob::F16Tile, 0)) {
         case 1: return launch_mfma16_cfg<128, 128, 64, 2, 2, 4, 16>(a, stream);
         case 2: return launch_mfma16_cfg<64, 64, 64, 2, 2, 4, 16>(a, stream);
         case 4: if (ring_ok) return launch_ring16_cfg<256, 128, 16>(a, stream); break;

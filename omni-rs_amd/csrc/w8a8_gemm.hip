@@ -1146,27 +1146,9 @@ __global__ __launch_bounds__(64 * NW, 1) void w8a8_ring_kernel(W8A8Args a, int s
     s_waitcnt_vm<0>();
 }
 
-// Compute units of the current device (cached per device).
-int num_cus() {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-            n = 256;
-        cached[dev] = n;
-    }
-    return cached[dev];
-}
-
 // OMNI_W8A8_TILE=<n> pins one tile configuration (tuning and test aid;
-// 0 or unset = the shape heuristic). Read on every launch so a process can
-// exercise each kernel variant in turn.
-int w8a8_tile_override() {
-    const char* v = std::getenv("OMNI_W8A8_TILE");
-    return v ? std::atoi(v) : 0;
-}
+// 0 or unset = the shape heuristic).
+int w8a8_tile_override() { return knob(Knob::W8A8Tile, 0); }
 
 template <int BN, int PF, bool KTAIL, bool OUT16, bool DUMP>
 hipError_t launch_cfg(const W8A8Args& a, hipStream_t stream) {
@@ -1391,12 +1373,9 @@ hipError_t launch_bn(const W8A8Args& a, hipStream_t stream) {
     return launch_out<BN, PF, false, false>(a, stream);
 }
 
-// OMNI_W8A8_SPLITS=<n> forces n-way split K on the pair ring (test aid;
-// read on every launch); 0 or unset = the shape rule below.
-int w8a8_split_override() {
-    const char* v = std::getenv("OMNI_W8A8_SPLITS");
-    return v ? std::atoi(v) : 0;
-}
+// OMNI_W8A8_SPLITS=<n> forces n-way split K on the pair ring (test aid);
+// 0 or unset = the shape rule below.
+int w8a8_split_override() { return knob(Knob::W8A8Splits, 0); }
 
 // Split K when 256 x 128 tiles fill at most half of the CUs and K >= 8192,
 // or at most an eighth of them and K >= 4096: K split up to 6 ways, at most

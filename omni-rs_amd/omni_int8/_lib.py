@@ -33,6 +33,7 @@ SIGNATURES = {
     "omni_int8_arch_supported": (_INT, [_INT]),
     "omni_w8a8_lowering": (_INT, [_I64]),
     "omni_int8_last_error": (ctypes.c_char_p, []),
+    "omni_int8_set_tuning": (_INT, [ctypes.c_char_p, _INT, _INT]),
     "omni_int8_quantize_rows": (_INT, [_P, _INT, _I64, _I64, _I64, _P, _P, _P, _P]),
     "omni_w8a8_gemm": (_INT, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _INT, _P, _INT, _P]),
     "omni_w8a8_gemm_workspace_size": (ctypes.c_size_t, [_I64, _I64, _I64]),

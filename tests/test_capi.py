@@ -94,3 +94,33 @@ def test_device_gate_without_gpu():
     p = ctypes.cast(dummy, ctypes.c_void_p)
     st = L.omni_int8_quantize_rows(p, 0, 1, 4, 4, p, p, p, None)
     assert st == _lib.OMNI_NO_DEVICE
+
+
+def test_tuning_knobs_set_unset_restore():
+    # omni_int8_set_tuning: modes 0 (environment), 1 (unset), 2 (value); an
+    # unknown name or mode is rejected; no GPU is involved.
+    L = _lib.lib()
+    for name in (b"OMNI_W8A8_TILE", b"OMNI_W8A16_SKINNY_SPLIT", b"OMNI_F16_TILE"):
+        assert L.omni_int8_set_tuning(name, 2, 17) == _lib.OMNI_OK
+        assert L.omni_int8_set_tuning(name, 1, 0) == _lib.OMNI_OK
+        assert L.omni_int8_set_tuning(name, 0, 0) == _lib.OMNI_OK
+    assert L.omni_int8_set_tuning(b"OMNI_NOT_A_KNOB", 2, 1) == _lib.OMNI_BAD_ARGUMENT
+    assert "unknown knob" in _lib.last_error()
+    assert L.omni_int8_set_tuning(b"OMNI_W8A8_TILE", 3, 1) == _lib.OMNI_BAD_ARGUMENT
+    assert L.omni_int8_set_tuning(None, 2, 1) == _lib.OMNI_BAD_ARGUMENT
+
+
+def test_no_getenv_on_launch_paths():
+    # The kernels' tuning knobs are read from the environment once per
+    # process (omni::knob); the only per-call reads are the reference's own
+    # switch OMNI_CONVROT_TENSOROPS (int8_tensorops.rs:15-20) and its
+    # companion OMNI_INT8_FORCE_SCALAR, plus OMNI_QWEN_TENSOROPS, read once.
+    csrc = os.path.join(ROOT, "omni-rs_amd", "csrc")
+    found = []
+    for name in sorted(os.listdir(csrc)):
+        text = open(os.path.join(csrc, name)).read()
+        found += [(name, arg) for arg in re.findall(r"getenv\(([^)]*)\)", text)]
+    assert sorted(found) == sorted([("capi.hip", '"OMNI_CONVROT_TENSOROPS"'),
+                                    ("capi.hip", '"OMNI_INT8_FORCE_SCALAR"'),
+                                    ("capi.hip", '"OMNI_QWEN_TENSOROPS"'),
+                                    ("capi.hip", "kKnobNames[i]")]), found

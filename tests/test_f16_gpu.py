@@ -88,10 +88,10 @@ def test_depth_probe_shapes(oracle, rows, k, n):
 
 
 @pytest.mark.parametrize("cfg", ["11", "12", "14", "18", "21", "22", "24", "41"])
-def test_gemv_every_configuration(oracle, monkeypatch, cfg):
+def test_gemv_every_configuration(oracle, monkeypatch, cfg, knobs):
     # OMNI_F16_GEMV pins one GEMV instantiation (chunks per lane, rows per
     # workgroup): each on ragged shapes up to its widest row (8192 * chunks).
-    monkeypatch.setenv("OMNI_F16_GEMV", cfg)
+    knobs.set("OMNI_F16_GEMV", cfg)
     widest = 8192 * int(cfg[0])
     for rows, k, n in ((1, widest, 77), (4, widest - 32, 9), (3, 1536, 130), (2, 32, 5)):
         rng = np.random.default_rng(rows + k + n + int(cfg))
@@ -151,13 +151,13 @@ def test_tensorops_shapes(oracle, rows, k, n):
 
 
 @pytest.mark.parametrize("tile", ["1", "2", "4", "5", "6", "7", "8", "10", "12", "13", "14"])
-def test_every_gemm_kernel(oracle, monkeypatch, tile):
+def test_every_gemm_kernel(oracle, monkeypatch, tile, knobs):
     # OMNI_F16_TILE pins one kernel: tiled 128 x 128 / 64 x 64, ring 256 x 128,
     # 128 x 128, 128 x 256, the 32-element-K-tile rings 256 x 256 and
     # 256 x 128, and the eight-wave rings 256 x 128 and 256 x 256 (32- and
     # 64-element K tiles; waves 64 x 128 or 128 x 64); ragged row counts and a
     # grid smaller than the CUs.
-    monkeypatch.setenv("OMNI_F16_TILE", tile)
+    knobs.set("OMNI_F16_TILE", tile)
     for rows, k, n in ((300, 4096, 4160), (1000, 4160, 4096), (256, 12288, 12288)):
         x, w = rand_operands(rows, k, n, rows * 3 + int(tile))
         got = tensorops_try_linear(x, w.t())

@@ -63,12 +63,12 @@ def test_every_path_random(oracle, rows, width, columns, group):
 
 
 @pytest.mark.parametrize("r", ["11", "21", "41", "81", "42", "44", "82"])
-def test_gemv_every_rows_per_workgroup(oracle, monkeypatch, r):
+def test_gemv_every_rows_per_workgroup(oracle, monkeypatch, r, knobs):
     # OMNI_W4A16_GEMV=<rows per batch><batches per workgroup>; column counts
     # leave the last workgroup's batches partly or wholly past the matrix;
     # one row at K = 4096 / 14336 with group 128 runs the kernels built for
     # those shapes
-    monkeypatch.setenv("OMNI_W4A16_GEMV", r)
+    knobs.set("OMNI_W4A16_GEMV", r)
     for rows, width, columns, group in ((1, 4096, 37, 32), (4, 2048, 130, 32), (3, 96, 9, 32),
                                         (1, 4096, 37, 128), (1, 14336, 21, 128)):
         rng = np.random.default_rng(rows + width + columns + int(r))
@@ -103,13 +103,13 @@ def test_guards():
                                                       (257, 8960, 129, 64), (197, 4096, 640, 256),
                                                       (65, 64, 33, 64), (600, 4096, 700, 128),
                                                       (130, 1536, 96, 32)])
-def test_every_prefill_kernel(oracle, monkeypatch, tile, rows, width, columns, group):
+def test_every_prefill_kernel(oracle, monkeypatch, tile, rows, width, columns, group, knobs):
     # OMNI_W4A16_TILE pins one prefill kernel: the tiled GEMMs (1, 2) and the
     # LDS-DMA rings on packed codes (4 = 256 x 128, 5 = 128 x 128, 6 = 256 x 256,
     # 10 = 128 x 128 two per CU, 16 / 17 / 18 = 128 x 256 / 256 x 256 /
     # 256 x 256 with eight waves; group 32 is not a ring case and takes the default); ragged
     # rows/columns, bias, against the f64 truth
-    monkeypatch.setenv("OMNI_W4A16_TILE", tile)
+    knobs.set("OMNI_W4A16_TILE", tile)
     rng = np.random.default_rng(rows + width + columns + group + int(tile))
     x, packed, bits, b = wd.random_case(rng, rows, width, columns, group, bias=True)
     got = run(x, packed, bits, b, group).astype(np.float64)
@@ -118,10 +118,10 @@ def test_every_prefill_kernel(oracle, monkeypatch, tile, rows, width, columns, g
 
 
 @pytest.mark.parametrize("tile", ["4", "5", "16", "17", "18"])
-def test_ring_integer_inputs_are_exact(monkeypatch, tile):
+def test_ring_integer_inputs_are_exact(monkeypatch, tile, knobs):
     # integer x and unit scales through the rings: every product and f32
     # partial sum is an exact integer, rounded once to f16 as the int64 product is
-    monkeypatch.setenv("OMNI_W4A16_TILE", tile)
+    knobs.set("OMNI_W4A16_TILE", tile)
     x = np.tile(np.arange(-4, 4, dtype=np.float16), (3, 64))[:, :512].copy()
     q = ((np.arange(70 * 512) % 7) - 3).reshape(70, 512)
     bits = wd.bf16_bits(np.ones((70, 4), np.float32))
@@ -133,11 +133,11 @@ def test_ring_integer_inputs_are_exact(monkeypatch, tile):
 
 
 @pytest.mark.parametrize("tile", ["0", "4", "18"])
-def test_scales_at_an_odd_bf16_offset(oracle, monkeypatch, tile):
+def test_scales_at_an_odd_bf16_offset(oracle, monkeypatch, tile, knobs):
     # The rings copy scales as 4-byte pairs; a scale array starting 2 bytes
     # past a 4-byte boundary (a contiguous view at an odd element) takes the
     # register-staged kernel instead, with the same result bar
-    monkeypatch.setenv("OMNI_W4A16_TILE", tile)
+    knobs.set("OMNI_W4A16_TILE", tile)
     rng = np.random.default_rng(int(tile) + 11)
     x, packed, bits, b = wd.random_case(rng, 300, 1024, 200, 128, bias=True)
     flat = np.concatenate([np.zeros(1, np.uint16), bits.reshape(-1)])
@@ -175,15 +175,15 @@ _SPLIT_CASES = {}
                                                            (300, 2048, 202, 64, True),
                                                            (130, 768, 515, 256, True),
                                                            (65, 128, 33, 64, False)])
-def test_split_k_every_ring(oracle, monkeypatch, tile, splits, rows, width, columns, group, bias):
+def test_split_k_every_ring(oracle, monkeypatch, tile, splits, rows, width, columns, group, bias, knobs):
     # OMNI_W4A16_SPLITS forces split K on a pinned int4 ring: units of
     # (tile, K range), f32 partial sums of the scaled codes, an in-order
     # reduction adding bias. K tile counts 64, 32, 12 and 2 (uneven splits,
     # fewer than asked when a split would be empty), ragged rows and columns,
     # columns % 4 != 0 (the reduction's scalar path); deterministic. One
     # case per shape, its f64 truth computed once.
-    monkeypatch.setenv("OMNI_W4A16_TILE", tile)
-    monkeypatch.setenv("OMNI_W4A16_SPLITS", splits)
+    knobs.set("OMNI_W4A16_TILE", tile)
+    knobs.set("OMNI_W4A16_SPLITS", splits)
     key = (rows, width, columns, group, bias)
     if key not in _SPLIT_CASES:
         rng = np.random.default_rng(rows + width + columns)
@@ -199,28 +199,28 @@ def test_split_k_every_ring(oracle, monkeypatch, tile, splits, rows, width, colu
     assert torch.equal(got, again), "split K must be deterministic"
 
 
-def test_split_k_workspace_contract(oracle, monkeypatch):
+def test_split_k_workspace_contract(oracle, monkeypatch, knobs):
     # omni_w4a16_gemm_workspace_size reports splits * rows * columns floats
     # for a split shape and 0 otherwise; omni_w4a16_gemm_ws splits less with
     # a smaller workspace, not at all with none, and every result is within
     # the bar.
     from omni_int8 import _lib
     L = _lib.lib()
-    monkeypatch.setenv("OMNI_W4A16_TILE", "4")
-    monkeypatch.setenv("OMNI_W4A16_SPLITS", "4")
+    knobs.set("OMNI_W4A16_TILE", "4")
+    knobs.set("OMNI_W4A16_SPLITS", "4")
     rows, width, columns, group = 300, 4096, 260, 128
     assert L.omni_w4a16_gemm_workspace_size(rows, columns, width, group) == 4 * rows * columns * 4
     assert L.omni_w4a16_gemm_workspace_size(64, columns, width, group) == 0  # skinny route
     assert L.omni_w4a16_gemm_workspace_size(4, columns, width, group) == 0  # GEMV
     assert L.omni_w4a16_gemm_workspace_size(rows, columns, width, 96) == 0  # width % group != 0
-    monkeypatch.delenv("OMNI_W4A16_TILE")
-    monkeypatch.delenv("OMNI_W4A16_SPLITS")
+    knobs.unset("OMNI_W4A16_TILE")
+    knobs.unset("OMNI_W4A16_SPLITS")
     # the launcher's own choice: MiniCPM-V's down projection at M = 1024
     # splits, its K = 3584 linears do not
     assert L.omni_w4a16_gemm_workspace_size(1024, 3584, 18944, 128) >= 2 * 1024 * 3584 * 4
     assert L.omni_w4a16_gemm_workspace_size(1024, 18944, 3584, 128) == 0
-    monkeypatch.setenv("OMNI_W4A16_TILE", "4")
-    monkeypatch.setenv("OMNI_W4A16_SPLITS", "4")
+    knobs.set("OMNI_W4A16_TILE", "4")
+    knobs.set("OMNI_W4A16_SPLITS", "4")
     rng = np.random.default_rng(79)
     x, packed, bits, b = wd.random_case(rng, rows, width, columns, group, bias=True)
     scale = torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).cuda()
@@ -237,7 +237,7 @@ def test_split_k_workspace_contract(oracle, monkeypatch):
         assert st == 0, _lib.last_error()
         assert tolerance.rel_err(out.cpu().numpy().astype(np.float64), truth) <= tolerance.FP16_REL_TOL, floats
         outs.append(out)
-    monkeypatch.setenv("OMNI_W4A16_SPLITS", "1")
+    knobs.set("OMNI_W4A16_SPLITS", "1")
     plain = oi.w4a16_linear(xd, pd, scale, bd, group=group)
     assert torch.equal(outs[2], plain), "no workspace runs unsplit"
     bad = torch.empty(1024, dtype=torch.uint8, device="cuda")
@@ -249,10 +249,10 @@ def test_split_k_workspace_contract(oracle, monkeypatch):
 @pytest.mark.parametrize("route", ["0", "1", "2"])
 @pytest.mark.parametrize("rows,width,columns,group", [(24, 4096, 8200, 128), (40, 2048, 16400, 64),
                                                       (40, 8192, 4100, 128), (17, 512, 300, 128)])
-def test_mid_rows_on_every_route(oracle, monkeypatch, route, rows, width, columns, group):
+def test_mid_rows_on_every_route(oracle, monkeypatch, route, rows, width, columns, group, knobs):
     # 17..64 activation rows: the default choice (the first two shapes take
     # the GEMM, the last two the skinny kernel), and each route forced
-    monkeypatch.setenv("OMNI_W8A16_ROUTE", route)
+    knobs.set("OMNI_W8A16_ROUTE", route)
     rng = np.random.default_rng(rows + width + columns + group)
     x, packed, bits, b = wd.random_case(rng, rows, width, columns, group, bias=True)
     got = run(x, packed, bits, b, group).astype(np.float64)
@@ -265,13 +265,13 @@ def test_mid_rows_on_every_route(oracle, monkeypatch, route, rows, width, column
                                                            (5, 4096, 300, 256, True), (12, 1024, 70, 128, False),
                                                            (16, 3072, 8199, 128, True), (7, 3584, 8300, 128, True),
                                                            (16, 1344, 600, 64, False)])
-def test_skinny_split_k(oracle, monkeypatch, splits, rows, width, columns, group, bias):
+def test_skinny_split_k(oracle, monkeypatch, splits, rows, width, columns, group, bias, knobs):
     # The int4 split-K skinny kernel (5..16 rows): units of 64 columns x
     # K / splits, partial sums of the scaled codes added in order by the
     # reduction (bias only); forced splits, and the default choice
     # ("auto": K of 3072..4096 over at least 8192 columns), deterministic
     if splits != "auto":
-        monkeypatch.setenv("OMNI_W4A16_SKINNY_SPLIT", splits)
+        knobs.set("OMNI_W4A16_SKINNY_SPLIT", splits)
     rng = np.random.default_rng(rows + width + columns + group)
     x, packed, bits, b = wd.random_case(rng, rows, width, columns, group, bias=bias)
     scale = torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).cuda()

@@ -66,13 +66,13 @@ def test_gemv_small_and_odd_shapes(oracle, rows, width, columns):
 
 @pytest.mark.parametrize("cfg", ["11", "12", "14", "18", "21", "22", "24",
                                  "142", "144", "124", "182", "242", "222"])
-def test_gemv_every_configuration(oracle, monkeypatch, cfg):
+def test_gemv_every_configuration(oracle, monkeypatch, cfg, knobs):
     # OMNI_W8A16_GEMV pins one GEMV instantiation (chunks per lane, rows per
     # batch, and batches per workgroup when there are three digits); each must
     # agree with the oracle on ragged shapes, including the widest row (16384),
     # a row narrower than one wavefront of chunks and column counts that leave
     # the last workgroup's batches partly or wholly past the matrix.
-    monkeypatch.setenv("OMNI_W8A16_GEMV", cfg)
+    knobs.set("OMNI_W8A16_GEMV", cfg)
     for rows, width, columns in ((1, 4096, 77), (4, 16384, 9), (3, 1536, 130), (2, 16, 5),
                                  (1, 14336, 31)):
         rng = np.random.default_rng(rows + width + columns + int(cfg))
@@ -145,12 +145,12 @@ def test_mfma_gemm_shapes(oracle, rows, width, columns):
 @pytest.mark.parametrize("rows,width,columns", [(5, 64, 33), (16, 4096, 4096), (13, 4112, 77),
                                                 (33, 1552, 200), (48, 16384, 17), (64, 8960, 1536),
                                                 (7, 16, 3), (40, 4096, 8200), (60, 2048, 8300)])
-def test_skinny_rows_on_both_routes(oracle, monkeypatch, route, rows, width, columns):
+def test_skinny_rows_on_both_routes(oracle, monkeypatch, route, rows, width, columns, knobs):
     # 5..64 activation rows: the default choice (route 0), the skinny MFMA
     # kernel (OMNI_W8A16_ROUTE=1) and the tiled MFMA GEMM (=2) against the
     # f64 ground truth, with K tails that are not a multiple of 64 and
     # ragged column counts; the last two shapes take the GEMM by default.
-    monkeypatch.setenv("OMNI_W8A16_ROUTE", route)
+    knobs.set("OMNI_W8A16_ROUTE", route)
     rng = np.random.default_rng(rows * 3 + width + columns)
     x, w, s, b = make(rng, rows, width, columns, bias=columns % 2 == 1)
     got = host(oi.w8a16_linear(dev(x), dev(w), dev(s), None if b is None else dev(b)))
@@ -162,12 +162,12 @@ def test_skinny_rows_on_both_routes(oracle, monkeypatch, route, rows, width, col
 @pytest.mark.parametrize("rows,width,columns", [(5, 64, 33), (8, 960, 70), (16, 4096, 4096),
                                                 (13, 2048, 17), (16, 4096, 129), (11, 4032, 300),
                                                 (7, 1024, 50), (14, 3072, 101), (16, 3136, 64)])
-def test_skinny_lds_kernel_and_fallback(oracle, monkeypatch, kernel, rows, width, columns):
+def test_skinny_lds_kernel_and_fallback(oracle, monkeypatch, kernel, rows, width, columns, knobs):
     # 5..16 rows with K % 64 == 0 and K <= 4096: the LDS-staged skinny kernel
     # (0; its K = 1024 / 2048 / 3072 / 4096 builds and the run-time-K one) and
     # w8a16_skinny_kernel (OMNI_W8A16_SKINNY=1), with idle waves (K < 1024),
     # ragged column counts and bias, against the f64 truth.
-    monkeypatch.setenv("OMNI_W8A16_SKINNY", kernel)
+    knobs.set("OMNI_W8A16_SKINNY", kernel)
     rng = np.random.default_rng(rows * 5 + width + columns)
     x, w, s, b = make(rng, rows, width, columns, bias=True)
     got = host(oi.w8a16_linear(dev(x), dev(w), dev(s), dev(b)))
@@ -178,14 +178,14 @@ def test_skinny_lds_kernel_and_fallback(oracle, monkeypatch, kernel, rows, width
 @pytest.mark.parametrize("tile", ["1", "2", "4", "5", "6", "7", "8", "9", "10", "11", "12", "16", "17", "18"])
 @pytest.mark.parametrize("rows,width,columns", [(300, 512, 200), (1024, 1536, 1536), (257, 8960, 129),
                                                 (197, 4096, 640), (65, 64, 33), (600, 4096, 700)])
-def test_every_prefill_kernel(oracle, monkeypatch, tile, rows, width, columns):
+def test_every_prefill_kernel(oracle, monkeypatch, tile, rows, width, columns, knobs):
     # OMNI_W8A16_TILE pins one prefill kernel: the tiled GEMMs (1, 2) and the
     # LDS-DMA ring GEMMs (4 = 256 x 128, 5 = 128 x 128, 6 = 256 x 256, 7 = 256 x 256
     # with the waves side by side, 8 = 64 x 128, 9 = 256 x 192, 10 = 128 x 128
     # two workgroups per CU, 11 / 12 = 64 x 128 two / three per CU, 16 / 17 /
     # 18 = 128 x 256 / 256 x 256 / 256 x 256 with eight waves); ragged
     # rows/columns, bias, against the f64 ground truth
-    monkeypatch.setenv("OMNI_W8A16_TILE", tile)
+    knobs.set("OMNI_W8A16_TILE", tile)
     rng = np.random.default_rng(rows + width + columns + int(tile))
     x, w, s, b = make(rng, rows, width, columns, bias=True)
     got = host(oi.w8a16_linear(dev(x), dev(w), dev(s), dev(b)))
@@ -210,14 +210,14 @@ def test_config5_small_vlm_layer(oracle):
 @pytest.mark.parametrize("rows,width,columns,bias", [(1024, 8960, 1536, False), (300, 1536, 202, True),
                                                      (257, 448, 129, True), (65, 64, 33, False),
                                                      (130, 4096, 515, True)])
-def test_split_k_every_ring_kernel(oracle, monkeypatch, tile, splits, rows, width, columns, bias):
+def test_split_k_every_ring_kernel(oracle, monkeypatch, tile, splits, rows, width, columns, bias, knobs):
     # OMNI_W8A16_SPLITS forces split K on a pinned ring kernel: units of
     # (tile, K range), f32 partial sums, an in-order reduction applying scale
     # and bias. K tile counts 140, 24, 7 (uneven splits, fewer than asked
     # when a split would be empty) and 1 (no split), ragged rows and
     # columns, columns % 4 != 0 (the reduction's scalar path).
-    monkeypatch.setenv("OMNI_W8A16_TILE", tile)
-    monkeypatch.setenv("OMNI_W8A16_SPLITS", splits)
+    knobs.set("OMNI_W8A16_TILE", tile)
+    knobs.set("OMNI_W8A16_SPLITS", splits)
     rng = np.random.default_rng(rows + width + columns + 10 * int(tile) + int(splits))
     x, w, s, b = make(rng, rows, width, columns, bias=bias)
     xd, wd, sd, bd = dev(x), dev(w), dev(s), None if b is None else dev(b)
@@ -228,21 +228,21 @@ def test_split_k_every_ring_kernel(oracle, monkeypatch, tile, splits, rows, widt
     assert torch.equal(got, again), "split K must be deterministic"
 
 
-def test_split_k_workspace_contract(monkeypatch):
+def test_split_k_workspace_contract(monkeypatch, knobs):
     # omni_w8a16_gemm_workspace_size reports splits * rows * columns floats
     # for a split shape and 0 otherwise; omni_w8a16_gemm_ws splits less with
     # a smaller workspace, not at all with none, and every result is within
     # the bar.
     from omni_int8 import _lib
     L = _lib.lib()
-    monkeypatch.setenv("OMNI_W8A16_TILE", "12")
-    monkeypatch.setenv("OMNI_W8A16_SPLITS", "4")
+    knobs.set("OMNI_W8A16_TILE", "12")
+    knobs.set("OMNI_W8A16_SPLITS", "4")
     rows, width, columns = 192, 2048, 256
     assert L.omni_w8a16_gemm_workspace_size(rows, columns, width) == 4 * rows * columns * 4
     assert L.omni_w8a16_gemm_workspace_size(64, columns, width) == 0  # skinny route
     assert L.omni_w8a16_gemm_workspace_size(4, columns, width) == 0  # GEMV
-    monkeypatch.delenv("OMNI_W8A16_TILE")
-    monkeypatch.delenv("OMNI_W8A16_SPLITS")
+    knobs.unset("OMNI_W8A16_TILE")
+    knobs.unset("OMNI_W8A16_SPLITS")
     # the launcher's own choice: config 5's down projection splits, its
     # K = 1536 linears do not
     assert L.omni_w8a16_gemm_workspace_size(1024, 1536, 8960) % (1024 * 1536 * 4) == 0
@@ -258,8 +258,8 @@ def test_split_k_workspace_contract(monkeypatch):
     assert st == 0, _lib.last_error()
     assert tolerance.rel_err(host(out), ref) <= tolerance.FP16_REL_TOL  # no workspace: unsplit
     assert tolerance.rel_err(host(oi.w8a16_linear(xd, wd, sd)), ref) <= tolerance.FP16_REL_TOL  # split
-    monkeypatch.setenv("OMNI_W8A16_TILE", "12")
-    monkeypatch.setenv("OMNI_W8A16_SPLITS", "4")
+    knobs.set("OMNI_W8A16_TILE", "12")
+    knobs.set("OMNI_W8A16_SPLITS", "4")
     rng = np.random.default_rng(77)
     x, w, s, b = make(rng, rows, width, columns, bias=True)
     xd, wd, sd, bd = dev(x), dev(w), dev(s), dev(b)
@@ -274,7 +274,7 @@ def test_split_k_workspace_contract(monkeypatch):
         assert st == 0, _lib.last_error()
         assert tolerance.rel_err(host(out), ref) <= tolerance.FP16_REL_TOL, floats
         outs.append(out)
-    monkeypatch.setenv("OMNI_W8A16_SPLITS", "1")
+    knobs.set("OMNI_W8A16_SPLITS", "1")
     plain = oi.w8a16_linear(xd, wd, sd, bd)
     assert torch.equal(outs[2], plain), "no workspace runs unsplit"
     bad = torch.empty(1024, dtype=torch.uint8, device="cuda")
@@ -288,13 +288,13 @@ def test_split_k_workspace_contract(monkeypatch):
                                                      (5, 8192, 300, True), (12, 256, 70, False),
                                                      (16, 1024, 4099, True), (13, 12288, 128, False),
                                                      (16, 3584, 8300, True), (8, 1344, 600, False)])
-def test_skinny_split_k(oracle, monkeypatch, splits, rows, width, columns, bias):
+def test_skinny_split_k(oracle, monkeypatch, splits, rows, width, columns, bias, knobs):
     # The decode-shaped split-K kernel (5..16 rows): units of 64 columns x
     # K / splits, f32 partial sums, then the in-order reduction. Splits that
     # do not divide K into multiples of 256 of at most 1024 fall back to the
     # unsplit kernels; ragged columns, bias, K from 256 to 12288.
     if splits != "auto":
-        monkeypatch.setenv("OMNI_W8A16_SKINNY_SPLIT", splits)
+        knobs.set("OMNI_W8A16_SKINNY_SPLIT", splits)
     rng = np.random.default_rng(rows * 7 + width + columns + (0 if splits == "auto" else int(splits)))
     x, w, s, b = make(rng, rows, width, columns, bias=bias)
     xd, wd, sd, bd = dev(x), dev(w), dev(s), None if b is None else dev(b)
@@ -303,7 +303,7 @@ def test_skinny_split_k(oracle, monkeypatch, splits, rows, width, columns, bias)
     ref = gpu_f64_reference(x, w, s, b)
     assert tolerance.rel_err(host(got), ref) <= tolerance.FP16_REL_TOL, (splits, rows, width, columns)
     assert torch.equal(got, again)
-    monkeypatch.setenv("OMNI_W8A16_SKINNY_SPLIT", "0")
+    knobs.set("OMNI_W8A16_SKINNY_SPLIT", "0")
     plain = oi.w8a16_linear(xd, wd, sd, bd)
     assert tolerance.rel_err(host(plain), ref) <= tolerance.FP16_REL_TOL
 

@@ -213,8 +213,8 @@ TILE_VARIANTS = [3, 4, 9, 10, 11, 12, 13, 14, 15, 16, 17, 19]  # OMNI_W8A8_TILE 
 
 
 @pytest.mark.parametrize("tile", [0] + TILE_VARIANTS)
-def test_w8a8_every_kernel_variant(oracle, tile, monkeypatch):
-    monkeypatch.setenv("OMNI_W8A8_TILE", str(tile))
+def test_w8a8_every_kernel_variant(oracle, tile, monkeypatch, knobs):
+    knobs.set("OMNI_W8A8_TILE", str(tile))
     for rows, width, columns in VARIANT_SHAPES:
         rng = np.random.default_rng(tile * 100 + rows)
         x = rng.standard_normal((rows, width)).astype(np.float16)
@@ -231,11 +231,11 @@ def test_w8a8_every_kernel_variant(oracle, tile, monkeypatch):
 
 
 @pytest.mark.parametrize("tile", [16, 17])
-def test_w8a8_pair_ring_short_and_odd_k(oracle, tile, monkeypatch):
+def test_w8a8_pair_ring_short_and_odd_k(oracle, tile, monkeypatch, knobs):
     # The pair-refill ring takes any K % 64 == 0: fewer K tiles than the ring
     # (1, 2, 3, 5), exactly one unrolled pass (10), one more (11), and odd
     # counts where a pair's second tile is clamped to the last one.
-    monkeypatch.setenv("OMNI_W8A8_TILE", str(tile))
+    knobs.set("OMNI_W8A8_TILE", str(tile))
     for rows, width, columns in [(300, 64, 700), (300, 128, 389), (513, 192, 700), (257, 320, 513),
                                  (1000, 640, 1500), (600, 704, 400), (520, 1344, 260)]:
         rng = np.random.default_rng(tile * 1000 + width)
@@ -260,13 +260,13 @@ def wrap_i32(t):
 
 
 @pytest.mark.parametrize("tile", [0] + TILE_VARIANTS)
-def test_w8a8_wide_row_sums_and_zero_points(oracle, tile, monkeypatch):
+def test_w8a8_wide_row_sums_and_zero_points(oracle, tile, monkeypatch, knobs):
     # The epilogue forms acc - row_sum * zero in 24-bit multiplies while every
     # row sum and zero point of a tile lies in [-2^23, 2^23), and in 32-bit
     # ones otherwise: caller-supplied sums and zero points at, inside and
     # outside that range (one wide row or column is enough to switch a whole
     # tile), with the product wrapping modulo 2^32 as int32 arithmetic does.
-    monkeypatch.setenv("OMNI_W8A8_TILE", str(tile))
+    knobs.set("OMNI_W8A8_TILE", str(tile))
     rows, width, columns = 600, 1024, 520
     rng = np.random.default_rng(400 + tile)
     codes = dev(rng.integers(-127, 128, (rows, width), dtype=np.int8))
@@ -296,9 +296,9 @@ def test_w8a8_wide_row_sums_and_zero_points(oracle, tile, monkeypatch):
 
 
 @pytest.mark.parametrize("tile", TILE_VARIANTS)
-def test_w8a8_every_kernel_variant_f16_bias(oracle, tile, monkeypatch):
+def test_w8a8_every_kernel_variant_f16_bias(oracle, tile, monkeypatch, knobs):
     # The f16-output and bias epilogue of each variant, on a ragged shape.
-    monkeypatch.setenv("OMNI_W8A8_TILE", str(tile))
+    knobs.set("OMNI_W8A8_TILE", str(tile))
     rows, width, columns = 700, 3072, 650
     rng = np.random.default_rng(tile)
     x = rng.standard_normal((rows, width)).astype(np.float16)
@@ -547,7 +547,7 @@ def test_w8a8_rejects_bad_vectors():
 
 
 @pytest.mark.parametrize("splits", [2, 3, 4, 8])
-def test_w8a8_split_k_bit_identical(oracle, splits, monkeypatch):
+def test_w8a8_split_k_bit_identical(oracle, splits, monkeypatch, knobs):
     # OMNI_W8A8_SPLITS forces split K on the 256 x 128 pair ring: int32
     # partial sums of (tile, K range) units, then a reduction applying the
     # epilogue. Every output (f32 and f16, bias, zero points or none, wide
@@ -555,7 +555,7 @@ def test_w8a8_split_k_bit_identical(oracle, splits, monkeypatch):
     # kernel's bit for bit; K tile counts 64, 24, 7 (uneven splits, fewer
     # than asked when a split would be empty) and 1 (no split), ragged rows
     # and columns, columns % 4 != 0 (the reduction's scalar path).
-    monkeypatch.setenv("OMNI_W8A8_TILE", "17")
+    knobs.set("OMNI_W8A8_TILE", "17")
     for rows, width, columns in [(256, 4096, 4096), (300, 1536, 202), (513, 448, 129), (70, 64, 33),
                                  (257, 4096, 515)]:
         rng = np.random.default_rng(splits * 1000 + width + columns)
@@ -571,10 +571,10 @@ def test_w8a8_split_k_bit_identical(oracle, splits, monkeypatch):
         for total, zero in (small, wide, (None, None)):
             for b in (None, bias):
                 for odt in (torch.float32, torch.float16):
-                    monkeypatch.delenv("OMNI_W8A8_SPLITS", raising=False)
+                    knobs.unset("OMNI_W8A8_SPLITS")
                     ref, ref_acc = oi.w8a8_gemm(codes, rs, total, w, scale, zero, bias=b, out_dtype=odt,
                                                 acc_dump=True, lowering=oi.OMNI_LOWERING_MFMA)
-                    monkeypatch.setenv("OMNI_W8A8_SPLITS", str(splits))
+                    knobs.set("OMNI_W8A8_SPLITS", str(splits))
                     got, acc = oi.w8a8_gemm(codes, rs, total, w, scale, zero, bias=b, out_dtype=odt,
                                             acc_dump=True, lowering=oi.OMNI_LOWERING_MFMA)
                     plain = oi.w8a8_gemm(codes, rs, total, w, scale, zero, bias=b, out_dtype=odt,
