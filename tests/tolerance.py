@@ -7,9 +7,31 @@ signed terms, so some land near zero where any change of summation order is
 an unbounded *relative* change (the reference's own GEMV/W4A16 tests floor
 their denominators too, crates/minicpm-v/src/quant.rs:313,552).
 """
+import os
+
 import numpy as np
 
 FP16_REL_TOL = 1e-2
+
+# The reference's own floor for its fp16 checks: |ref|.max(0.1)
+# (crates/minicpm-v/src/quant.rs:552), whose Metal FP16 route it holds to
+# 5e-2 (:556).
+REF_CLAMP = 0.1
+
+# (test, rms-floored error, error under the reference's clamp) of every
+# rel_err call in this session, summarised by conftest.py at the end.
+RECORD = []
+
+
+def ref_clamp_err(got, ref):
+    """max |got - ref| / max(|ref|, 0.1): the reference's own measure."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    if ref.size == 0:
+        return 0.0
+    if not np.all(np.isfinite(got)):
+        return float("inf")
+    return float(np.max(np.abs(got - ref) / np.maximum(np.abs(ref), REF_CLAMP)))
 
 
 def rel_err(got, ref):
@@ -21,4 +43,6 @@ def rel_err(got, ref):
         return float("inf")
     rms = float(np.sqrt(np.mean(ref * ref)))
     floor = max(0.1 * rms, 1e-30)
-    return float(np.max(np.abs(got - ref) / np.maximum(np.abs(ref), floor)))
+    err = float(np.max(np.abs(got - ref) / np.maximum(np.abs(ref), floor)))
+    RECORD.append((os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0], err, ref_clamp_err(got, ref)))
+    return err
