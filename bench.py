@@ -294,6 +294,74 @@ def reference_shape_context(torch, oi, dev, stream, steps):
     return res
 
 
+# Algorithmic bytes of the decode GEMV rows the read ceiling is measured for
+# (M=1; weights + scales + activations + outputs): W8A16 4096 x 4096, W4A16
+# 4096 -> 14336 (group 128), W8A16 4096 -> 14336 (the headline GEMV).
+READ_CEILING_ROWS = (
+    ("w8a16 M=1 4096x4096", 4096 * 4096 + 2 * 4096 + 2 * 4096 + 2 * 4096),
+    ("w4a16 M=1 4096x14336", 14336 * 4096 // 2 + 2 * 14336 * 32 + 2 * 4096 + 2 * 14336),
+    ("w8a16 M=1 4096x14336", 14336 * 4096 + 2 * 14336 + 2 * 4096 + 2 * 14336),
+)
+
+
+def hbm_read_ceiling(torch, gen, dev, stream, steps):
+    """What one launch can stream from HBM at the decode GEMVs' byte counts:
+    a bare read of the same number of bytes (libomni_read_ceiling.so: every
+    nontemporal 16-byte load of a thread issued before any is used, nothing
+    computed or written), over copies rotated past the 256 MB MALL like the
+    GEMV rows, at nine launch shapes (1, 2 or 4 loads per thread; 256, 512 or
+    1024 threads per block); the fastest shape is the ceiling. Outside every
+    timed step."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "omni-rs_amd", "libomni_read_ceiling.so"))
+    lib.omni_read_ceiling.restype = ctypes.c_int
+    lib.omni_read_ceiling.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_uint32,
+                                      ctypes.c_void_p, ctypes.c_void_p]
+    shapes = [(u, t) for u in (1, 2, 4) for t in (256, 512, 1024)]
+    assert lib.omni_read_ceiling_shapes() == len(shapes)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    rows = []
+    for label, nbytes in READ_CEILING_ROWS:
+        padded = -(-nbytes // 16) * 16
+        copies = max(4, -(-GEMV_ROTATION_BYTES // padded))
+        bufs = [torch.randint(-128, 128, (padded,), generator=gen, device=dev, dtype=torch.int8)
+                for _ in range(copies)]
+        times = []
+        for shape in range(len(shapes)):
+            idx = [0]
+
+            def one(shape=shape):
+                b = bufs[idx[0] % copies]
+                idx[0] += 1
+                st = lib.omni_read_ceiling(b.data_ptr(), padded, shape, 0x9E3779B9, sink.data_ptr(),
+                                           torch.cuda.current_stream(dev).cuda_stream)
+                assert st == 0, st
+
+            for _ in range(copies):
+                one()
+            iters = copies * max(1, steps // 8)
+            g = graph_of(one, iters)
+            times.append(timed_graph(g, stream) / iters)
+            del g
+        del bufs
+        best = min(range(len(shapes)), key=lambda i: times[i])
+        t = times[best]
+        rows.append({"row": label, "bytes": nbytes, "copies": copies, "us": round(t * 1e6, 3),
+                     "GB/s": round(nbytes / t / 1e9, 1), "hbm_frac": round(nbytes / t / 1e9 / PEAK_HBM_GBS, 4),
+                     "loads_per_thread": shapes[best][0], "block": shapes[best][1],
+                     "all_shapes_us": [round(x * 1e6, 2) for x in times]})
+    return rows
+
+
+def read_ceiling_frac(ceiling, nbytes, us):
+    """A GEMV row's time against the bare read of the same bytes (null when
+    the ceiling was not measured at that byte count)."""
+    for r in ceiling:
+        if r["bytes"] == nbytes:
+            return round(r["us"] / us, 4)
+    return None
+
+
 def w4a16_bench(torch, oi, gen, dev, stream, steps):
     """Weight-only int4 GEMV (group 128, bf16 scales) at M=1 on the W8A16
     headline shape K=4096, N=14336, over weight copies rotated past the MALL:
@@ -779,6 +847,12 @@ def main():
     # ---- W4A16 GEMV (MiniCPM-V pack-quantized int4) --------------------------
     w4 = w4a16_bench(torch, oi, gen, dev, stream, args.steps)
 
+    # ---- HBM read ceiling at the GEMV rows' byte counts ----------------------
+    mark(torch, "hbm_read_ceiling")
+    ceiling = hbm_read_ceiling(torch, gen, dev, stream, args.steps)
+    w4["frac_of_read_ceiling"] = read_ceiling_frac(
+        ceiling, READ_CEILING_ROWS[1][1], w4["us_per_launch"])
+
     # ---- fp16 analogs: depth GEMV and DiT GEMM -------------------------------
     f16_res = f16_bench(torch, gen, dev, stream, args.steps)
 
@@ -787,6 +861,9 @@ def main():
 
     # ---- every BASELINE.json config ----------------------------------------------
     configs_res = configs_bench(torch, oi, gen, dev, stream, args.steps)
+    for r in configs_res.get("2_gemv_sweep", []):
+        nb = r["N"] * r["K"] + 2 * r["N"] + 2 * r["M"] * r["K"] + 2 * r["M"] * r["N"]
+        r["frac_of_read_ceiling"] = read_ceiling_frac(ceiling, nb, r["us"])
 
     # ---- CPU baselines (oracle, bounded samples) -----------------------------
     import oracle_lib
@@ -824,11 +901,13 @@ def main():
             "config": {"M": gM, "K": gK, "N": gN, "weight_copies": copies,
                        "rotation_bytes": copies * gN * gK},
             "us_per_launch": round(t_gemv * 1e6, 3),
+            "frac_of_read_ceiling": read_ceiling_frac(ceiling, gemv_bytes, t_gemv * 1e6),
             "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": round(gemv_gbs / PEAK_HBM_GBS, 4),
                          "traffic": traffic.get("w8a16_gemv")},
             "cpu_baseline": cpu_gemv,
         },
+        "hbm_read_ceiling": ceiling,
         "convrot": convrot_res,
         "w4a16_gemv": w4,
         "f16": f16_res,
