@@ -22,8 +22,10 @@ OMNI_LOWERING_AUTO = 0
 OMNI_LOWERING_MFMA = 1
 OMNI_LOWERING_SCALAR = 2
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
-                        "libomni_int8.so")
+# OMNI_INT8_LIBRARY may name another build of the same library (the
+# host-sanitised one that tests/sanitize_cpu.sh runs the CPU tests on).
+LIB_PATH = os.environ.get("OMNI_INT8_LIBRARY") or os.path.join(
+    os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "libomni_int8.so")
 
 # name -> (restype, argtypes); one entry per declaration in include/omni_int8.h
 _P = ctypes.c_void_p

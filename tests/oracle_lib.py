@@ -9,7 +9,8 @@ import os
 import numpy as np
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB = os.path.join(ROOT, "oracle", "liboracle_int8.so")
+# OMNI_ORACLE_LIBRARY may name the sanitised build (tests/sanitize_cpu.sh).
+LIB = os.environ.get("OMNI_ORACLE_LIBRARY") or os.path.join(ROOT, "oracle", "liboracle_int8.so")
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int64
