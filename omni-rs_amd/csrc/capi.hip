@@ -115,15 +115,22 @@ int w8a16_route() { return omni::knob(omni::Knob::W8A16Route, 0); }
 // 4096 -> 14336: 24.5 against 37.7 us at 24 rows, 27.4 against 70.5 at 64;
 // 4096 -> 4096 stays skinny to 48 rows: 15.5 against 16.8). W4A16 over a
 // long K (14336 -> 4096) stays skinny to 48 rows (40.3 against 43.4 at 32).
-bool midrows_take_gemm(int64_t rows, int64_t columns, int64_t width, bool int4) {
+// Those GEMM times are the ring kernels'. Where no ring can run (K % 64 !=
+// 0 and the like) the register-staged GEMM takes only more than 48 rows of
+// at least 32 M weights (W8A16 K = 4112: 48 x 9000 39.2 us skinny against
+// 43.4, 24 x 16000 36.3 against 42.5, 64 x 12000 51.8 against 43.5).
+bool midrows_take_gemm(int64_t rows, int64_t columns, int64_t width, bool int4, bool ring_ok) {
     const double elems = (double)columns * (double)width;
+    if (!ring_ok) return rows > 48 && elems >= 32e6;
     if (rows > 48 && elems >= 16e6) return true;
     if (int4 && columns < 2 * width) return false;
     return elems >= 32e6;
 }
 
-// The W8A16 route: 0 GEMV, 1 skinny MFMA, 2 the GEMM.
-int w8a16_kind(int64_t rows, int64_t columns, int64_t width) {
+// The W8A16 route: 0 GEMV, 1 skinny MFMA, 2 the GEMM. `a` gives the shape
+// (and, for W4A16, the group and scale layout) the ring check reads.
+int w8a16_kind(const omni::W8A16Args& a) {
+    const int64_t rows = a.rows, columns = a.columns, width = a.width;
     // The GEMV spreads a row over one workgroup of at most 1024 lanes, one
     // 16-element chunk per lane: width <= 16384.
     if (rows <= 4 && width <= 16384) return 0;
@@ -133,17 +140,28 @@ int w8a16_kind(int64_t rows, int64_t columns, int64_t width) {
     const int r = w8a16_route();
     if (r == 1) return 1;
     if (r == 2) return 2;
-    return rows > 16 && midrows_take_gemm(rows, columns, width, false) ? 2 : 1;
+    return rows > 16 && midrows_take_gemm(rows, columns, width, false, omni::w8a16_ring_usable(a)) ? 2 : 1;
 }
 
 // The same for W4A16 (its GEMV takes width <= 32768).
-int w4a16_kind(int64_t rows, int64_t columns, int64_t width) {
+int w4a16_kind(const omni::W8A16Args& a) {
+    const int64_t rows = a.rows, columns = a.columns, width = a.width;
     if (rows <= 4 && width <= 32768) return 0;
     if (rows > 64) return 2;
     const int r = w8a16_route();
     if (r == 1) return 1;
     if (r == 2) return 2;
-    return rows > 16 && midrows_take_gemm(rows, columns, width, true) ? 2 : 1;
+    return rows > 16 && midrows_take_gemm(rows, columns, width, true, omni::w4a16_ring_usable(a)) ? 2 : 1;
+}
+
+// The shape fields of W8A16Args (no pointers: the size queries).
+omni::W8A16Args shape_args(int64_t rows, int64_t columns, int64_t width, int64_t group = 0) {
+    omni::W8A16Args a{};
+    a.rows = rows;
+    a.columns = columns;
+    a.width = width;
+    a.group = group;
+    return a;
 }
 
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
@@ -567,7 +585,7 @@ int omni_convrot_linear(const void* x, int x_dtype, int64_t rows, int64_t width,
 
 size_t omni_w8a16_gemm_workspace_size(int64_t rows, int64_t columns, int64_t width) {
     if (rows <= 0 || columns <= 0 || width <= 0 || width % 16 != 0) return 0;
-    switch (w8a16_kind(rows, columns, width)) {
+    switch (w8a16_kind(shape_args(rows, columns, width))) {
         case 1: return (size_t)omni::w8a16_skinny_partial_elems(rows, columns, width) * sizeof(float);
         case 2: return (size_t)omni::w8a16_partial_elems(rows, columns, width) * sizeof(float);
         default: return 0;
@@ -608,7 +626,7 @@ int omni_w8a16_gemm_ws(const uint16_t* x, const int8_t* w, const uint16_t* scale
     a.partial = static_cast<float*>(workspace);
     a.partial_elems = (int64_t)(workspace_bytes / sizeof(float));
     hipStream_t s = static_cast<hipStream_t>(stream);
-    switch (w8a16_kind(rows, columns, width)) {
+    switch (w8a16_kind(a)) {
         case 0: return hip_status(omni::launch_w8a16_gemv(a, s), "w8a16 gemv launch");
         case 1: return hip_status(omni::launch_w8a16_skinny(a, s), "w8a16 skinny launch");
         default: return hip_status(omni::launch_w8a16_mfma(a, s), "w8a16 mfma launch");
@@ -619,7 +637,7 @@ size_t omni_w4a16_gemm_workspace_size(int64_t rows, int64_t columns, int64_t wid
     if (rows <= 0 || columns <= 0 || width <= 0 || group <= 0 || width % 32 != 0 || group % 32 != 0 ||
         width % group != 0)
         return 0;
-    switch (w4a16_kind(rows, columns, width)) {
+    switch (w4a16_kind(shape_args(rows, columns, width, group))) {
         case 1: return (size_t)omni::w4a16_skinny_partial_elems(rows, columns, width) * sizeof(float);
         case 2: return (size_t)omni::w4a16_partial_elems(rows, columns, width, group) * sizeof(float);
         default: return 0;
@@ -667,7 +685,7 @@ int omni_w4a16_gemm_ws(const uint16_t* x, const uint8_t* w_packed, const uint16_
     a.partial = static_cast<float*>(workspace);
     a.partial_elems = (int64_t)(workspace_bytes / sizeof(float));
     hipStream_t s = static_cast<hipStream_t>(stream);
-    switch (w4a16_kind(rows, columns, width)) {
+    switch (w4a16_kind(a)) {
         case 0: return hip_status(omni::launch_w4a16_gemv(a, s), "w4a16 gemv launch");
         case 1: return hip_status(omni::launch_w4a16_skinny(a, s), "w4a16 skinny launch");
         default: return hip_status(omni::launch_w4a16_mfma(a, s), "w4a16 mfma launch");

@@ -77,6 +77,12 @@ struct W8A16Args {
     int64_t partial_elems = 0;          // floats available at `partial`
 };
 
+// Whether an LDS-DMA ring GEMM can run this shape (int8, int4: also the
+// group and scale layout); without one launch_w8a16_mfma and
+// launch_w4a16_mfma take the register-staged tiled kernels.
+bool w8a16_ring_usable(const W8A16Args& a);
+bool w4a16_ring_usable(const W8A16Args& a);
+
 hipError_t launch_w8a16_gemv(const W8A16Args& a, hipStream_t stream);
 hipError_t launch_w8a16_skinny(const W8A16Args& a, hipStream_t stream);
 hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream);

@@ -2209,4 +2209,7 @@ hipError_t launch_f16_mfma(const W8A16Args& a, hipStream_t stream) {
     return launch_mfma16_cfg<64, 64, 64, 2, 2, 4, 16>(a, stream);
 }
 
+bool w8a16_ring_usable(const W8A16Args& a) { return ring16_fits(a); }
+bool w4a16_ring_usable(const W8A16Args& a) { return w4_ring_ok(a); }
+
 }  // namespace omni

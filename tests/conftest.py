@@ -61,14 +61,14 @@ def pytest_terminal_summary(terminalreporter):
     if not tolerance.RECORD:
         return
     worst = {}
-    for test, err, clamp in tolerance.RECORD:
-        f = test.split("::")[0]
-        w = worst.setdefault(f, [0, 0.0, 0.0, ""])
+    for test, truth, err, clamp in tolerance.RECORD:
+        key = (test.split("::")[0], "f64 truth" if truth else "other rounded routes")
+        w = worst.setdefault(key, [0, 0.0, 0.0, ""])
         w[0] += 1
         w[1] = max(w[1], err)
         if clamp > w[2]:
             w[2], w[3] = clamp, test
     terminalreporter.write_sep("-", "fp16 output errors (max per file)")
-    for f, (n, err, clamp, where) in sorted(worst.items()):
-        terminalreporter.write_line(f"{f}: {n} checks, rms-floored {err:.3e}, "
+    for (f, against), (n, err, clamp, where) in sorted(worst.items()):
+        terminalreporter.write_line(f"{f} vs {against}: {n} checks, rms-floored {err:.3e}, "
                                     f"|ref|.max(0.1) {clamp:.3e} at {where}")

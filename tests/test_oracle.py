@@ -238,11 +238,11 @@ def test_w8a16_gemm_exact_on_integers_and_within_tolerance(oracle):
     s = rng.uniform(0.002, 0.02, 64).astype(np.float16)
     ref = oracle.w8a16_f64(x, w, s)
     got = oracle.w8a16_gemm(x, w, s).astype(np.float64)
-    assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL
+    assert tolerance.rel_err(got, ref, truth=False) <= tolerance.FP16_REL_TOL
     # negative control: a 2% scale error on one channel must fail the bar
     bad = got.copy()
     bad[:, 5] *= 1.02
-    assert tolerance.rel_err(bad, ref) > tolerance.FP16_REL_TOL
+    assert tolerance.rel_err(bad, ref, truth=False) > tolerance.FP16_REL_TOL
 
 
 # -- ConvRot Hadamard (convrot.rs:121-149, tests :169-220) -----------------------

@@ -59,7 +59,7 @@ def test_every_path_random(oracle, rows, width, columns, group):
     truth = oracle.w4a16_f64(x, packed, bits, group, b)
     assert tolerance.rel_err(got, truth) <= tolerance.FP16_REL_TOL, (rows, width, columns, group)
     route = oracle.w4a16_gemm(x, packed, bits, group, b).astype(np.float64)
-    assert tolerance.rel_err(got, route) <= tolerance.FP16_REL_TOL
+    assert tolerance.rel_err(got, route, truth=False) <= tolerance.FP16_REL_TOL
 
 
 @pytest.mark.parametrize("r", ["11", "21", "41", "81", "42", "44", "82"])
