@@ -1279,7 +1279,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, i
     static_assert(kRows % (16 * NW) == 0 && FM >= 1 && FN >= 1 && WMW * WNW == NW, "tile shape");
     static_assert(kCpw <= 2 * FM * FN && kFrags <= 2 * FM * FN, "one read and copy per MFMA slot");
     static_assert((S - 1) * kOps < 64, "ops in flight within vmcnt");
-    static_assert(WB != 4 || (KP == 2 && FM >= 2 && BN % 64 == 0), "int4 ring shape");
+    static_assert(WB != 4 || (KP == 2 && FM >= 2 && BN % 64 == 0 && BN <= 64 * NW), "int4 ring shape");
     // int4 and int8 codes: converted ahead, spread over the previous pair's
     // MFMA slots (int8: 3-16 % faster than converting at the start of the
     // pair on the four-wave and the eight-wave 256 x 256 rings, MI355X).
@@ -1317,7 +1317,13 @@ __global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, i
     unsigned voff[kCpw];
     unsigned voff_sc = 0;  // int4: this lane's scale column, byte offset of its row
     int64_t m0 = 0, n0 = 0;
-    float p_sc = 0.0f, p_bi = 0.0f;
+    // A tile's column scales and biases, held between their load and their
+    // store into the idle parameter buffer: kPP per thread, as BN may exceed
+    // the workgroup's 64 * NW threads (column tid + 64 NW i for slot i).
+    constexpr int kPP = (BN + 64 * NW - 1) / (64 * NW);
+    float p_sc[kPP], p_bi[kPP];
+#pragma unroll
+    for (int i = 0; i < kPP; ++i) p_sc[i] = p_bi[i] = 0.0f;
     auto tile_origin = [&](int u, int64_t& tm0, int64_t& tn0) {
         const int l = SK ? u % total : u;
         const int group_size = kGroupM * tiles_n;
@@ -1376,16 +1382,24 @@ __global__ __launch_bounds__(64 * NW, OCC) void w8a16_ring_kernel(W8A16Args a, i
         }
     };
     auto load_params = [&](int64_t pn0) {
-        if (tid < BN) {
-            const int64_t col = min(pn0 + tid, a.columns - 1);
-            p_sc = WB == 8 ? (float)a.scale[col] : 1.0f;
-            p_bi = has_bias ? (float)a.bias[col] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < kPP; ++i) {
+            const int c = tid + 64 * NW * i;
+            if (c < BN) {
+                const int64_t col = min(pn0 + c, a.columns - 1);
+                p_sc[i] = WB == 8 ? (float)a.scale[col] : 1.0f;
+                p_bi[i] = has_bias ? (float)a.bias[col] : 0.0f;
+            }
         }
     };
     auto store_params = [&](int par) {
-        if (tid < BN) {
-            sScale[par][tid] = p_sc;
-            sBias[par][tid] = p_bi;
+#pragma unroll
+        for (int i = 0; i < kPP; ++i) {
+            const int c = tid + 64 * NW * i;
+            if (c < BN) {
+                sScale[par][c] = p_sc[i];
+                sBias[par][c] = p_bi[i];
+            }
         }
     };
     auto unit_k = [&](int u) {
@@ -1828,8 +1842,8 @@ hipError_t launch_w8a16_skinny(const W8A16Args& a, hipStream_t stream) { return 
 // 256 x 256 (2 x 2 waves), 7 = ring 256 x 256 (1 x 4 waves), 8 = ring
 // 64 x 128, 9 = ring 256 x 192, 10 = ring 128 x 128 two workgroups per CU,
 // 11 / 12 = ring 64 x 128 two / three per CU, 16 / 17 / 18 = ring 128 x 256 /
-// 256 x 256 (waves 64 x 128) / 256 x 256 (waves 128 x 64) with eight waves
-// (rings: K % 64 == 0 only). OMNI_W8A16_SPLITS=<n>
+// 256 x 256 (waves 64 x 128) / 256 x 256 (waves 128 x 64) with eight waves,
+// 19 = ring 128 x 320 (rings: K % 64 == 0 only). OMNI_W8A16_SPLITS=<n>
 // adds n-way split K to a pinned ring (or to the shape rule's choice) when
 // the call brings a workspace. Both are tuning knobs (omni::knob).
 int w8a16_tile_override() { return knob(Knob::W8A16Tile, 0); }
@@ -1848,7 +1862,7 @@ W16Plan plan_w8a16(const W8A16Args& a, int cus, bool ws_limited) {
     const int split_override = knob(Knob::W8A16Splits, 0);
     const bool ring_ok = ring16_fits(a);
     const int ov = w8a16_tile_override();
-    if (ov == 1 || ov == 2 || (ov >= 4 && ov <= 12 && ring_ok) || (ov >= 16 && ov <= 18 && ring_ok))
+    if (ov == 1 || ov == 2 || (ov >= 4 && ov <= 12 && ring_ok) || (ov >= 16 && ov <= 19 && ring_ok))
         return {ov, ov >= 4 && split_override > 1 ? split_override : 1};
     if (!ring_ok) {
         const int64_t big_tiles = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
@@ -1895,8 +1909,16 @@ W16Plan plan_w8a16(const W8A16Args& a, int cus, bool ws_limited) {
     // The 256 x 256 candidate is then the eight-wave ring with two waves
     // along M (each 128 x 64, half the conversions per MFMA of the 64 x 128
     // one): 0.93-0.96 of that one's time on five shapes, so 0.95 of its fit.)
+    // 128 x 320 (four waves of 64 x 160; 2 BM + BN = 9 x 64 stage rows, so
+    // the copies divide over the waves) gives the M = 1024 and 2048 shapes
+    // 8 x 28 / 16 x 28 tiles where 256 x 192 leaves a quarter of the CUs idle
+    // (1024 x 1536 -> 8960: 188 tiles): fitted on MI355X at K = 1536 and
+    // 4096 (1024 x K -> 8960: 36.8 / 79.1 us), it changes the pick on eight
+    // of 38 swept shapes, each 5-13 % faster (1024 x 1536 -> 17920: 72.5
+    // against 83.8 us), and on no other.
     Cand best = cost(18, 0.3184, 358.8, 256, 256);
-    for (const Cand& c : {cost(9, 0.3846, 359.2, 256, 192), cost(16, 0.4289, 201.6, 128, 256)})
+    for (const Cand& c : {cost(9, 0.3846, 359.2, 256, 192), cost(16, 0.4289, 201.6, 128, 256),
+                          cost(19, 0.4186, 291.4, 128, 320)})
         if (c.t < best.t) best = c;
     // At most half a round of tiles and K >= 8192: split that ring's tiles
     // 2-4 ways to about one unit per CU (1024 x 18944 -> 3584: 128 x 256
@@ -1950,6 +1972,7 @@ hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream) {
         case 16: return launch_ring16_cfg<128, 256, 8, 2, 3, 2, 1, 8>(a, stream, sp);
         case 17: return launch_ring16_cfg<256, 256, 8, 4, 3, 2, 1, 8>(a, stream, sp);
         case 18: return launch_ring16_cfg<256, 256, 8, 2, 3, 2, 1, 8>(a, stream, sp);
+        case 19: return launch_ring16_cfg<128, 320>(a, stream, sp);
         default: return launch_ring16_cfg<64, 128, 8, 2, 3, 2, 3>(a, stream, sp);
     }
 }

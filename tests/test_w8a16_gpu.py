@@ -179,7 +179,8 @@ def test_skinny_lds_kernel_and_fallback(oracle, monkeypatch, kernel, rows, width
     assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL, (kernel, rows, width, columns)
 
 
-@pytest.mark.parametrize("tile", ["1", "2", "4", "5", "6", "7", "8", "9", "10", "11", "12", "16", "17", "18"])
+@pytest.mark.parametrize("tile", ["1", "2", "4", "5", "6", "7", "8", "9", "10", "11", "12", "16", "17", "18",
+                                  "19"])
 @pytest.mark.parametrize("rows,width,columns", [(300, 512, 200), (1024, 1536, 1536), (257, 8960, 129),
                                                 (197, 4096, 640), (65, 64, 33), (600, 4096, 700)])
 def test_every_prefill_kernel(oracle, monkeypatch, tile, rows, width, columns, knobs):
@@ -187,8 +188,10 @@ def test_every_prefill_kernel(oracle, monkeypatch, tile, rows, width, columns, k
     # LDS-DMA ring GEMMs (4 = 256 x 128, 5 = 128 x 128, 6 = 256 x 256, 7 = 256 x 256
     # with the waves side by side, 8 = 64 x 128, 9 = 256 x 192, 10 = 128 x 128
     # two workgroups per CU, 11 / 12 = 64 x 128 two / three per CU, 16 / 17 /
-    # 18 = 128 x 256 / 256 x 256 / 256 x 256 with eight waves); ragged
-    # rows/columns, bias, against the f64 ground truth
+    # 18 = 128 x 256 / 256 x 256 / 256 x 256 with eight waves, 19 = 128 x 320,
+    # whose tile has more columns than the workgroup has threads, so each
+    # thread stages two columns' scale and bias); ragged rows/columns, bias,
+    # against the f64 ground truth
     knobs.set("OMNI_W8A16_TILE", tile)
     rng = np.random.default_rng(rows + width + columns + int(tile))
     x, w, s, b = make(rng, rows, width, columns, bias=True)
@@ -209,7 +212,7 @@ def test_config5_small_vlm_layer(oracle):
             assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL, (rows, width, columns)
 
 
-@pytest.mark.parametrize("tile", ["4", "5", "8", "9", "10", "11", "12", "16", "17", "18"])
+@pytest.mark.parametrize("tile", ["4", "5", "8", "9", "10", "11", "12", "16", "17", "18", "19"])
 @pytest.mark.parametrize("splits", ["2", "3", "5", "8"])
 @pytest.mark.parametrize("rows,width,columns,bias", [(1024, 8960, 1536, False), (300, 1536, 202, True),
                                                      (257, 448, 129, True), (65, 64, 33, False),
