@@ -1843,7 +1843,8 @@ hipError_t launch_w8a16_skinny(const W8A16Args& a, hipStream_t stream) { return 
 // 64 x 128, 9 = ring 256 x 192, 10 = ring 128 x 128 two workgroups per CU,
 // 11 / 12 = ring 64 x 128 two / three per CU, 16 / 17 / 18 = ring 128 x 256 /
 // 256 x 256 (waves 64 x 128) / 256 x 256 (waves 128 x 64) with eight waves,
-// 19 = ring 128 x 320 (rings: K % 64 == 0 only). OMNI_W8A16_SPLITS=<n>
+// 19 / 20 / 21 = ring 128 x 320 / 64 x 192 / 128 x 192 (rings: K % 64 == 0
+// only). OMNI_W8A16_SPLITS=<n>
 // adds n-way split K to a pinned ring (or to the shape rule's choice) when
 // the call brings a workspace. Both are tuning knobs (omni::knob).
 int w8a16_tile_override() { return knob(Knob::W8A16Tile, 0); }
@@ -1862,7 +1863,7 @@ W16Plan plan_w8a16(const W8A16Args& a, int cus, bool ws_limited) {
     const int split_override = knob(Knob::W8A16Splits, 0);
     const bool ring_ok = ring16_fits(a);
     const int ov = w8a16_tile_override();
-    if (ov == 1 || ov == 2 || (ov >= 4 && ov <= 12 && ring_ok) || (ov >= 16 && ov <= 19 && ring_ok))
+    if (ov == 1 || ov == 2 || (ov >= 4 && ov <= 12 && ring_ok) || (ov >= 16 && ov <= 21 && ring_ok))
         return {ov, ov >= 4 && split_override > 1 ? split_override : 1};
     if (!ring_ok) {
         const int64_t big_tiles = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
@@ -1877,6 +1878,17 @@ W16Plan plan_w8a16(const W8A16Args& a, int cus, bool ws_limited) {
     // 1536 the partial sums' traffic costs more than the split saves.
     const int64_t tiles64 = ((a.rows + 63) / 64) * ((a.columns + 127) / 128);
     if (a.width >= 4096 && tiles64 < cus) {
+        // K >= 8192 with as many 128 x 192 tiles as divide the CUs 2-4 ways:
+        // those tiles split that many ways fill every CU exactly once
+        // (config 5's down projection, 1024 x 8960 -> 1536: 64 tiles, four
+        // splits, 40.9 us against 45.9 on 128 x 128 tiles split two ways; on
+        // K = 4096, or splits that leave CUs idle, the rule below wins).
+        const int64_t tiles192 = ((a.rows + 127) / 128) * ((a.columns + 191) / 192);
+        if (a.width >= 8192 && split_override <= 1 && cus % tiles192 == 0) {
+            const int sp = (int)(cus / tiles192);
+            if (sp >= 2 && sp <= 4 && (!ws_limited || fit_splits(a, (int)(a.width / 64), sp) == sp))
+                return {21, sp};
+        }
         const int64_t tiles128 = ((a.rows + 127) / 128) * ((a.columns + 127) / 128);
         const int64_t want = cus / tiles128;
         const int sp = split_override > 1 ? split_override : (int)(want < 2 ? 2 : want > 4 ? 4 : want);
@@ -1973,6 +1985,8 @@ hipError_t launch_w8a16_mfma(const W8A16Args& a, hipStream_t stream) {
         case 17: return launch_ring16_cfg<256, 256, 8, 4, 3, 2, 1, 8>(a, stream, sp);
         case 18: return launch_ring16_cfg<256, 256, 8, 2, 3, 2, 1, 8>(a, stream, sp);
         case 19: return launch_ring16_cfg<128, 320>(a, stream, sp);
+        case 20: return launch_ring16_cfg<64, 192>(a, stream, sp);
+        case 21: return launch_ring16_cfg<128, 192>(a, stream, sp);
         default: return launch_ring16_cfg<64, 128, 8, 2, 3, 2, 3>(a, stream, sp);
     }
 }

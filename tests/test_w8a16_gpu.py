@@ -180,7 +180,7 @@ def test_skinny_lds_kernel_and_fallback(oracle, monkeypatch, kernel, rows, width
 
 
 @pytest.mark.parametrize("tile", ["1", "2", "4", "5", "6", "7", "8", "9", "10", "11", "12", "16", "17", "18",
-                                  "19"])
+                                  "19", "20", "21"])
 @pytest.mark.parametrize("rows,width,columns", [(300, 512, 200), (1024, 1536, 1536), (257, 8960, 129),
                                                 (197, 4096, 640), (65, 64, 33), (600, 4096, 700)])
 def test_every_prefill_kernel(oracle, monkeypatch, tile, rows, width, columns, knobs):
@@ -190,8 +190,8 @@ def test_every_prefill_kernel(oracle, monkeypatch, tile, rows, width, columns, k
     # two workgroups per CU, 11 / 12 = 64 x 128 two / three per CU, 16 / 17 /
     # 18 = 128 x 256 / 256 x 256 / 256 x 256 with eight waves, 19 = 128 x 320,
     # whose tile has more columns than the workgroup has threads, so each
-    # thread stages two columns' scale and bias); ragged rows/columns, bias,
-    # against the f64 ground truth
+    # thread stages two columns' scale and bias, 20 / 21 = 64 x 192 /
+    # 128 x 192); ragged rows/columns, bias, against the f64 ground truth
     knobs.set("OMNI_W8A16_TILE", tile)
     rng = np.random.default_rng(rows + width + columns + int(tile))
     x, w, s, b = make(rng, rows, width, columns, bias=True)
@@ -212,7 +212,7 @@ def test_config5_small_vlm_layer(oracle):
             assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL, (rows, width, columns)
 
 
-@pytest.mark.parametrize("tile", ["4", "5", "8", "9", "10", "11", "12", "16", "17", "18", "19"])
+@pytest.mark.parametrize("tile", ["4", "5", "8", "9", "10", "11", "12", "16", "17", "18", "19", "20", "21"])
 @pytest.mark.parametrize("splits", ["2", "3", "5", "8"])
 @pytest.mark.parametrize("rows,width,columns,bias", [(1024, 8960, 1536, False), (300, 1536, 202, True),
                                                      (257, 448, 129, True), (65, 64, 33, False),
@@ -265,6 +265,16 @@ def test_split_k_workspace_contract(monkeypatch, knobs):
     assert st == 0, _lib.last_error()
     assert tolerance.rel_err(host(out), ref) <= tolerance.FP16_REL_TOL  # no workspace: unsplit
     assert tolerance.rel_err(host(oi.w8a16_linear(xd, wd, sd)), ref) <= tolerance.FP16_REL_TOL  # split
+    # the plan asks for four splits of 128 x 192 tiles there; with room for
+    # three or two it takes 128 x 128 tiles split two ways instead
+    assert L.omni_w8a16_gemm_workspace_size(1024, 1536, 8960) == 4 * 1024 * 1536 * 4
+    for floats in (4 * 1024 * 1536, 3 * 1024 * 1536, 2 * 1024 * 1536):
+        ws = torch.empty(floats * 4, dtype=torch.uint8, device="cuda")
+        ws.fill_(0x5A)
+        st = L.omni_w8a16_gemm_ws(xd.data_ptr(), wd.data_ptr(), sd.data_ptr(), None, 1024, 1536, 8960,
+                                  out.data_ptr(), ws.data_ptr(), floats * 4, torch.cuda.current_stream().cuda_stream)
+        assert st == 0, _lib.last_error()
+        assert tolerance.rel_err(host(out), ref) <= tolerance.FP16_REL_TOL, floats
     knobs.set("OMNI_W8A16_TILE", "12")
     knobs.set("OMNI_W8A16_SPLITS", "4")
     rng = np.random.default_rng(77)
