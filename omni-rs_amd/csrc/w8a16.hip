@@ -834,23 +834,31 @@ hipError_t launch_skinny(const W8A16Args& a, hipStream_t stream) {
 // load is issued up front. KF > 0 and GF > 0 build the kernel for K == KF,
 // a multiple of 2048 (every lane then owns one chunk), and group == GF: no
 // clamp, and the scale index without a 64-bit division.
-template <int MR, int R, int B = 1, int KF = 0, int GF = 0>
-__global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W8A16Args a) {
+// TEAMS > 1 (K == KF builds only): the workgroup holds TEAMS teams of
+// T = KF / 32 lanes, team t taking the R * B rows after team t - 1's, so a
+// 2-wave team's rows share a workgroup (and its launch) with the next team's
+// (MI355X, 4096 x 4096: 3.71 against 3.88 us with one team of 4 rows). KF
+// builds are bounded by their exact workgroup size.
+template <int MR, int R, int B = 1, int KF = 0, int GF = 0, int TEAMS = 1>
+__global__ __launch_bounds__(KF > 0 ? KF / 32 * TEAMS : 1024) void w4a16_gemv_kernel(W8A16Args a) {
     constexpr int V = R * MR;
-    constexpr int RB = R * B;  // rows per workgroup: B batches of R
+    constexpr int RB = R * B;  // rows per team: B batches of R
     static_assert((V & (V - 1)) == 0 && V <= 64, "power-of-two partial count");
     static_assert(KF % 2048 == 0 && (KF == 0) == (GF == 0), "KF: a multiple of 2048, with GF");
+    static_assert(TEAMS == 1 || (KF > 0 && KF / 32 * TEAMS <= 1024), "teams: K == KF builds within 1024 lanes");
     __shared__ float s_part[16][B * V];
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int T = KF > 0 ? KF / 32 : (int)blockDim.x;
+    const int team = TEAMS > 1 ? tid / T : 0;
+    const int tt = TEAMS > 1 ? tid - team * T : tid;  // lane within the team
     const int64_t K = KF > 0 ? KF : a.width;
     const int64_t group = GF > 0 ? GF : a.group;
     const int64_t chunks = K / 32;
     const int64_t gpr = K / group;  // scale groups per weight row
-    const int64_t n0 = (int64_t)blockIdx.x * RB;
-    const bool live = KF > 0 || tid < chunks;
-    const int64_t c = live ? tid : chunks - 1;  // clamped: meets zero activations
+    const int64_t n0 = ((int64_t)blockIdx.x * TEAMS + team) * RB;
+    const bool live = KF > 0 || tt < chunks;
+    const int64_t c = live ? tt : chunks - 1;  // clamped: meets zero activations
 
     // x: 32 halves of each row's chunk as 16 f16 pairs, in the order of
     // i4x8_to_f16x8_biased's weight pairs: (x0, x2), (x1, x3), (x4, x6),
@@ -860,42 +868,23 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W8A16Args a) {
     // weight row, so they pay when a lane has more weight rows than
     // activation rows; otherwise x keeps its order and codes are exact.
     constexpr bool kBiased = RB > MR;
-    v2h xr[MR][16];
-    float xc[MR];
-    const v2h k1032 = {(_Float16)1032.0f, (_Float16)1032.0f};
+    // Every load goes out before any arithmetic: x's raw chunks (rows past
+    // a.rows read row 0, zeroed below, so no load sits in a branch), then the
+    // group scales, then the weights. (With x loaded and re-paired inside a
+    // per-row branch, the generated code waited for x before issuing a single
+    // weight load; MI355X, 4096 x 4096: 3.88 against 4.15 us, 4 rows at
+    // 4096 x 14336: 13.0 against 14.35, 14336 x 4096: 8.5 against 8.3.) The scales come
+    // before the weights because memory operations retire in order: a scale
+    // issued after every weight row would hold row 0's arithmetic until the
+    // last row had landed.
+    uint4 xq[MR][4];
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
-        if (live && m < a.rows) {
-            const uint4* p = reinterpret_cast<const uint4*>(a.x + m * K + c * 32);
+        const int64_t mr = m < a.rows ? m : 0;
+        const uint4* p = reinterpret_cast<const uint4*>(a.x + mr * K + c * 32);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint4 v = p[q];
-                if constexpr (kBiased) {
-                    xr[m][4 * q] = bits_half2(__builtin_amdgcn_perm(v.y, v.x, 0x05040100u));
-                    xr[m][4 * q + 1] = bits_half2(__builtin_amdgcn_perm(v.y, v.x, 0x07060302u));
-                    xr[m][4 * q + 2] = bits_half2(__builtin_amdgcn_perm(v.w, v.z, 0x05040100u));
-                    xr[m][4 * q + 3] = bits_half2(__builtin_amdgcn_perm(v.w, v.z, 0x07060302u));
-                } else {
-                    xr[m][4 * q] = bits_half2(v.x);
-                    xr[m][4 * q + 1] = bits_half2(v.y);
-                    xr[m][4 * q + 2] = bits_half2(v.z);
-                    xr[m][4 * q + 3] = bits_half2(v.w);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) xr[m][e] = v2h{};
-        }
-        xc[m] = 0.0f;
-        if constexpr (kBiased) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) xc[m] = __builtin_amdgcn_fdot2(k1032, xr[m][e], xc[m], false);
-        }
+        for (int q = 0; q < 4; ++q) xq[m][q] = p[q];
     }
-    const u32 k64 = 0x64646464u;
-    // The group scales are loaded before the weights: memory operations
-    // retire in order, so a scale issued after every weight row would hold
-    // row 0's arithmetic until the last row had landed.
     v4u wv[RB];
     float sc[RB];
 #pragma unroll
@@ -908,7 +897,36 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W8A16Args a) {
         const int64_t n = n0 + r < a.columns ? n0 + r : a.columns - 1;
         wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(a.w + n * (K / 2) + c * 16));
     }
-    const int64_t n_ep = min(n0 + (tid / MR) % RB, a.columns - 1);
+    __builtin_amdgcn_sched_barrier(0);
+    v2h xr[MR][16];
+    float xc[MR];
+    const v2h k1032 = {(_Float16)1032.0f, (_Float16)1032.0f};
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        const bool keep = live && m < a.rows;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint4 v = keep ? xq[m][q] : make_uint4(0, 0, 0, 0);
+            if constexpr (kBiased) {
+                xr[m][4 * q] = bits_half2(__builtin_amdgcn_perm(v.y, v.x, 0x05040100u));
+                xr[m][4 * q + 1] = bits_half2(__builtin_amdgcn_perm(v.y, v.x, 0x07060302u));
+                xr[m][4 * q + 2] = bits_half2(__builtin_amdgcn_perm(v.w, v.z, 0x05040100u));
+                xr[m][4 * q + 3] = bits_half2(__builtin_amdgcn_perm(v.w, v.z, 0x07060302u));
+            } else {
+                xr[m][4 * q] = bits_half2(v.x);
+                xr[m][4 * q + 1] = bits_half2(v.y);
+                xr[m][4 * q + 2] = bits_half2(v.z);
+                xr[m][4 * q + 3] = bits_half2(v.w);
+            }
+        }
+        xc[m] = 0.0f;
+        if constexpr (kBiased) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) xc[m] = __builtin_amdgcn_fdot2(k1032, xr[m][e], xc[m], false);
+        }
+    }
+    const u32 k64 = 0x64646464u;
+    const int64_t n_ep = min(n0 + (tt / MR) % RB, a.columns - 1);
     const _Float16 bi_h = a.bias ? a.bias[n_ep] : (_Float16)0.0f;
 
 #pragma unroll
@@ -940,12 +958,12 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W8A16Args a) {
     if ((lane & (64 / V - 1)) == 0) s_part[wave][b * V + fold_index<V>(lane)] = part[0];
     }
     __syncthreads();
-    if (tid < B * V) {
-        const int r = tid / MR, m = tid % MR;
+    if (tt < B * V) {
+        const int r = tt / MR, m = tt % MR;
         const int64_t n = n0 + r;
         if (n < a.columns && m < a.rows) {
             float acc = 0.0f;
-            for (int w = 0; w < T / 64; ++w) acc += s_part[w][tid];
+            for (int w = 0; w < T / 64; ++w) acc += s_part[team * (T / 64) + w][tt];
             a.out[(int64_t)m * a.columns + n] = (_Float16)(acc + (float)bi_h);
         }
     }
@@ -2006,6 +2024,15 @@ hipError_t launch_w4a16_gemv(const W8A16Args& a, hipStream_t stream) {
     // 14336 x 4096, 3 rows: 13.0 against 14.5; 4096 x 4096 stays on 4 rows,
     // 6.3 against 7.9).
     const int64_t code_bytes = a.columns * a.width / 2;
+    // One row at K = 4096, group 128, from 4 MB of codes: two 128-lane teams
+    // of 8 rows per workgroup (MI355X, weights rotated past the MALL, against
+    // one team of 4 or 2 x 4 rows: 4096 x 4096 3.71 against 3.88 us, 4096 x
+    // 14336 7.65-7.7 against 7.85, the 128256-row head 41.4-41.8 against 42.2).
+    if (cfg == 0 && a.rows == 1 && a.group == 128 && a.width == 4096 && code_bytes >= (4 << 20)) {
+        const dim3 grid((unsigned)((a.columns + 15) / 16)), block(256);
+        hipLaunchKernelGGL((w4a16_gemv_kernel<1, 8, 1, 4096, 128, 2>), grid, block, 0, stream, a);
+        return hipGetLastError();
+    }
     if (cfg == 0) {
         if (code_bytes >= (64 << 20)) cfg = 42;
         else if (a.rows >= 2 && code_bytes >= (16 << 20)) cfg = 81;

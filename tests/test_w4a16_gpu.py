@@ -78,6 +78,20 @@ def test_gemv_every_rows_per_workgroup(oracle, monkeypatch, r, knobs):
         assert tolerance.rel_err(got, truth) <= tolerance.FP16_REL_TOL, (r, rows, width, columns)
 
 
+@pytest.mark.parametrize("columns", [2048, 2051, 2056, 2063, 14336])
+def test_gemv_two_team_build(oracle, columns):
+    # one row at K = 4096, group 128, from 4 MB of codes: two 128-lane teams
+    # of 8 rows per workgroup; the last workgroup's second team lies partly
+    # (2051, 2063) or wholly (2056) past the matrix
+    rng = np.random.default_rng(columns)
+    x, packed, bits, b = wd.random_case(rng, 1, 4096, columns, 128, bias=True)
+    got = run(x, packed, bits, b, 128).astype(np.float64)
+    truth = oracle.w4a16_f64(x, packed, bits, 128, b)
+    assert tolerance.rel_err(got, truth) <= tolerance.FP16_REL_TOL, columns
+    route = oracle.w4a16_gemm(x, packed, bits, 128, b).astype(np.float64)
+    assert tolerance.rel_err(got, route, truth=False) <= tolerance.FP16_REL_TOL, columns
+
+
 def test_integer_inputs_are_exact():
     # integer x and unit scales: every partial sum is an integer below 2^11
     x = np.tile(np.arange(-4, 4, dtype=np.float16), (3, 32))[:, :256].copy()
