@@ -1731,31 +1731,78 @@ bool ring16_fits(const W8A16Args& a) {
 
 // Split-K reduction: out[r][c] = f16((sum over s in order of partial[s][r][c])
 // * scale[c] + bias[c]), four consecutive elements per lane.
+// S > 0 builds the kernel for exactly S splits: every partial load, and the
+// four columns' scales and biases, go out before the first add (with the
+// split count read at run time each add waited on its own load: config 5's
+// down projection, four splits, 7.2 us). The adds keep split order.
+template <int S = 0>
 __global__ __launch_bounds__(256) void w8a16_split_reduce_kernel(W8A16Args a, int splits) {
     const int64_t n = a.rows * a.columns;
     const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= n) return;
     float v[4];
     int e_end = 4;
-    if (a.columns % 4 == 0) {
-        float4 s = *reinterpret_cast<const float4*>(a.partial + i);
-        for (int p = 1; p < splits; ++p) {
-            const float4 t = *reinterpret_cast<const float4*>(a.partial + p * n + i);
-            s.x += t.x;
-            s.y += t.y;
-            s.z += t.z;
-            s.w += t.w;
-        }
-        v[0] = s.x, v[1] = s.y, v[2] = s.z, v[3] = s.w;
-    } else {
-        e_end = (int)min((int64_t)4, n - i);
-        for (int e = 0; e < e_end; ++e) {
-            float s = a.partial[i + e];
-            for (int p = 1; p < splits; ++p) s += a.partial[p * n + i + e];
-            v[e] = s;
-        }
-    }
     int64_t c = i % a.columns;
+    if (a.columns % 4 == 0) {
+        // The four elements are consecutive columns c .. c + 3 of one row.
+        // Scale and bias are loaded unconditionally (from the partial sums,
+        // in range, where a pointer is null: int4 weights are scaled in the
+        // kernel), so that no load sits in a branch that waits for it.
+        const bool has_sc = a.scale != nullptr, has_bi = a.bias != nullptr;
+        const _Float16* sp = has_sc ? a.scale : reinterpret_cast<const _Float16*>(a.partial);
+        const _Float16* bp = has_bi ? a.bias : reinterpret_cast<const _Float16*>(a.partial);
+        _Float16 sh[4], bh[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            sh[e] = sp[c + e];
+            bh[e] = bp[c + e];
+        }
+        float4 s;
+        if constexpr (S > 0) {
+            float4 t[S];
+#pragma unroll
+            for (int p = 0; p < S; ++p) t[p] = *reinterpret_cast<const float4*>(a.partial + p * n + i);
+            s = t[0];
+#pragma unroll
+            for (int p = 1; p < S; ++p) {
+                s.x += t[p].x;
+                s.y += t[p].y;
+                s.z += t[p].z;
+                s.w += t[p].w;
+            }
+        } else {
+            s = *reinterpret_cast<const float4*>(a.partial + i);
+            for (int p = 1; p < splits; ++p) {
+                const float4 t = *reinterpret_cast<const float4*>(a.partial + p * n + i);
+                s.x += t.x;
+                s.y += t.y;
+                s.z += t.z;
+                s.w += t.w;
+            }
+        }
+        const float r[4] = {s.x, s.y, s.z, s.w};
+        _Float16 o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float sc = has_sc ? (float)sh[e] : 1.0f;
+            const float bi = has_bi ? (float)bh[e] : 0.0f;
+            o[e] = (_Float16)(r[e] * sc + bi);
+        }
+        if (reinterpret_cast<uintptr_t>(a.out + i) % 8 == 0) {
+            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+            *reinterpret_cast<h4*>(a.out + i) = h4{o[0], o[1], o[2], o[3]};
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a.out[i + e] = o[e];
+        }
+        return;
+    }
+    e_end = (int)min((int64_t)4, n - i);
+    for (int e = 0; e < e_end; ++e) {
+        float s = a.partial[i + e];
+        for (int p = 1; p < splits; ++p) s += a.partial[p * n + i + e];
+        v[e] = s;
+    }
     _Float16 o[4];
     for (int e = 0; e < e_end; ++e) {
         if (e > 0 && ++c == a.columns) c = 0;
@@ -1763,12 +1810,24 @@ __global__ __launch_bounds__(256) void w8a16_split_reduce_kernel(W8A16Args a, in
         const float bi = a.bias ? (float)a.bias[c] : 0.0f;
         o[e] = (_Float16)(v[e] * sc + bi);
     }
-    if (e_end == 4 && reinterpret_cast<uintptr_t>(a.out + i) % 8 == 0) {
-        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-        *reinterpret_cast<h4*>(a.out + i) = h4{o[0], o[1], o[2], o[3]};
-        return;
-    }
     for (int e = 0; e < e_end; ++e) a.out[i + e] = o[e];
+}
+
+// The reduction launch: the build for exactly `splits` splits from 2 to 8.
+hipError_t launch_split_reduce(const W8A16Args& a, int splits, hipStream_t stream) {
+    const int64_t quads = (a.rows * a.columns + 3) / 4;
+    const dim3 grid((unsigned)((quads + 255) / 256)), block(256);
+    switch (splits) {
+        case 2: hipLaunchKernelGGL((w8a16_split_reduce_kernel<2>), grid, block, 0, stream, a, splits); break;
+        case 3: hipLaunchKernelGGL((w8a16_split_reduce_kernel<3>), grid, block, 0, stream, a, splits); break;
+        case 4: hipLaunchKernelGGL((w8a16_split_reduce_kernel<4>), grid, block, 0, stream, a, splits); break;
+        case 5: hipLaunchKernelGGL((w8a16_split_reduce_kernel<5>), grid, block, 0, stream, a, splits); break;
+        case 6: hipLaunchKernelGGL((w8a16_split_reduce_kernel<6>), grid, block, 0, stream, a, splits); break;
+        case 7: hipLaunchKernelGGL((w8a16_split_reduce_kernel<7>), grid, block, 0, stream, a, splits); break;
+        case 8: hipLaunchKernelGGL((w8a16_split_reduce_kernel<8>), grid, block, 0, stream, a, splits); break;
+        default: hipLaunchKernelGGL((w8a16_split_reduce_kernel<0>), grid, block, 0, stream, a, splits);
+    }
+    return hipGetLastError();
 }
 
 template <int WB>
@@ -1781,10 +1840,7 @@ hipError_t launch_skinny_split(const W8A16Args& a, int splits, hipStream_t strea
         hipLaunchKernelGGL((w8a16_skinny_split_kernel<WB>), dim3((unsigned)units), dim3(1024), 0, stream, a, splits);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int64_t quads = (a.rows * a.columns + 3) / 4;
-    hipLaunchKernelGGL(w8a16_split_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, a,
-                       splits);
-    return hipGetLastError();
+    return launch_split_reduce(a, splits, stream);
 }
 
 int cu_count() { return num_cus(); }
@@ -1816,10 +1872,7 @@ hipError_t launch_ring16_cfg(const W8A16Args& a, hipStream_t stream, int splits 
                                dim3(64 * NW), 0, stream, a, splits);
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
-            const int64_t quads = (a.rows * a.columns + 3) / 4;
-            hipLaunchKernelGGL(w8a16_split_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0,
-                               stream, a, splits);
-            return hipGetLastError();
+            return launch_split_reduce(a, splits, stream);
         }
     }
     const int64_t grid = tiles < slots ? tiles : slots;
