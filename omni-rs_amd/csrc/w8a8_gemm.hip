@@ -1208,34 +1208,73 @@ hipError_t launch_ring_cfg(const W8A8Args& a, hipStream_t stream) {
 // any order), then the ring's epilogue, four consecutive elements per lane:
 // out = f32(acc - x_sum * w_zero) * x_scale * w_scale (+ bias), as f32 or
 // rounded once to f16; the accumulators to acc_dump when asked.
-template <bool OUT16, bool DUMP>
+// S > 0 builds the kernel for exactly S splits. With columns % 4 == 0 (the
+// four elements then lie in one row) every load, the partial sums and the
+// epilogue's row and column parameters, goes out before the first add: the
+// parameters are read unconditionally (from another in-range array where a
+// pointer is null) and selected afterwards, as a load in a branch would be
+// waited for in that branch. The arithmetic is the same either way.
+template <bool OUT16, bool DUMP, int S = 0>
 __global__ __launch_bounds__(256) void w8a8_split_reduce_kernel(W8A8Args a, int splits) {
     const int64_t n = a.rows * a.columns;
     const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= n) return;
     unsigned v[4] = {0u, 0u, 0u, 0u};
     int e_end = 4;
+    const bool has_zero = a.w_zero != nullptr;
+    int64_t row = i / a.columns, col = i - row * a.columns;
+    float o[4];
     if (a.columns % 4 == 0) {
-        for (int p = 0; p < splits; ++p) {
-            const int4 t = *reinterpret_cast<const int4*>(a.partial + p * n + i);
-            v[0] += (unsigned)t.x;
-            v[1] += (unsigned)t.y;
-            v[2] += (unsigned)t.z;
-            v[3] += (unsigned)t.w;
+        const bool has_bias = a.bias != nullptr;
+        const int32_t* xs_p = has_zero ? a.x_sum : reinterpret_cast<const int32_t*>(a.x_scale);
+        const int32_t* wz_p = has_zero ? a.w_zero : reinterpret_cast<const int32_t*>(a.w_scale);
+        const float* bi_p = has_bias ? a.bias : a.w_scale;
+        const float rs = a.x_scale[row];
+        const unsigned xs = (unsigned)xs_p[row];
+        float ws[4], bi[4];
+        unsigned wz[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            ws[e] = a.w_scale[col + e];
+            wz[e] = (unsigned)wz_p[col + e];
+            bi[e] = bi_p[col + e];
+        }
+        if constexpr (S > 0) {
+            int4 t[S];
+#pragma unroll
+            for (int p = 0; p < S; ++p) t[p] = *reinterpret_cast<const int4*>(a.partial + p * n + i);
+#pragma unroll
+            for (int p = 0; p < S; ++p) {
+                v[0] += (unsigned)t[p].x;
+                v[1] += (unsigned)t[p].y;
+                v[2] += (unsigned)t[p].z;
+                v[3] += (unsigned)t[p].w;
+            }
+        } else {
+            for (int p = 0; p < splits; ++p) {
+                const int4 t = *reinterpret_cast<const int4*>(a.partial + p * n + i);
+                v[0] += (unsigned)t.x;
+                v[1] += (unsigned)t.y;
+                v[2] += (unsigned)t.z;
+                v[3] += (unsigned)t.w;
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const unsigned prod = has_zero ? xs * wz[e] : 0u;
+            const int centered = (int)(v[e] - prod);
+            o[e] = w8a8_scale(centered, rs, ws[e], has_bias ? bi[e] : -0.0f);
         }
     } else {
         e_end = (int)min((int64_t)4, n - i);
         for (int e = 0; e < e_end; ++e)
             for (int p = 0; p < splits; ++p) v[e] += (unsigned)a.partial[p * n + i + e];
-    }
-    const bool has_zero = a.w_zero != nullptr;
-    int64_t row = i / a.columns, col = i - row * a.columns;
-    float o[4];
-    for (int e = 0; e < e_end; ++e) {
-        if (e > 0 && ++col == a.columns) col = 0, ++row;
-        const unsigned prod = has_zero ? (unsigned)a.x_sum[row] * (unsigned)a.w_zero[col] : 0u;
-        const int centered = (int)(v[e] - prod);
-        o[e] = w8a8_scale(centered, a.x_scale[row], a.w_scale[col], a.bias ? a.bias[col] : -0.0f);
+        for (int e = 0; e < e_end; ++e) {
+            if (e > 0 && ++col == a.columns) col = 0, ++row;
+            const unsigned prod = has_zero ? (unsigned)a.x_sum[row] * (unsigned)a.w_zero[col] : 0u;
+            const int centered = (int)(v[e] - prod);
+            o[e] = w8a8_scale(centered, a.x_scale[row], a.w_scale[col], a.bias ? a.bias[col] : -0.0f);
+        }
     }
     // Whole 16-byte (8-byte) stores when aligned: four 4-byte nontemporal
     // stores into one line were written back to HBM separately.
@@ -1289,8 +1328,16 @@ hipError_t launch_pair_split(const W8A8Args& a, int splits, hipStream_t stream) 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int64_t quads = (a.rows * a.columns + 3) / 4;
-    hipLaunchKernelGGL((w8a8_split_reduce_kernel<OUT16, DUMP>), dim3((unsigned)((quads + 255) / 256)), dim3(256), 0,
-                       stream, a, splits);
+    const dim3 rgrid((unsigned)((quads + 255) / 256)), rblock(256);
+    switch (splits) {
+        case 2: hipLaunchKernelGGL((w8a8_split_reduce_kernel<OUT16, DUMP, 2>), rgrid, rblock, 0, stream, a, splits); break;
+        case 3: hipLaunchKernelGGL((w8a8_split_reduce_kernel<OUT16, DUMP, 3>), rgrid, rblock, 0, stream, a, splits); break;
+        case 4: hipLaunchKernelGGL((w8a8_split_reduce_kernel<OUT16, DUMP, 4>), rgrid, rblock, 0, stream, a, splits); break;
+        case 5: hipLaunchKernelGGL((w8a8_split_reduce_kernel<OUT16, DUMP, 5>), rgrid, rblock, 0, stream, a, splits); break;
+        case 6: hipLaunchKernelGGL((w8a8_split_reduce_kernel<OUT16, DUMP, 6>), rgrid, rblock, 0, stream, a, splits); break;
+        case 8: hipLaunchKernelGGL((w8a8_split_reduce_kernel<OUT16, DUMP, 8>), rgrid, rblock, 0, stream, a, splits); break;
+        default: hipLaunchKernelGGL((w8a8_split_reduce_kernel<OUT16, DUMP>), rgrid, rblock, 0, stream, a, splits);
+    }
     return hipGetLastError();
 }
 
