@@ -719,7 +719,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the path shards by output columns across GPUs, see DESIGN.md)", file=sys.stderr)
+              "(across GPUs the path would shard by output columns, one GPU's share being this "
+              "same kernel at N/gpus columns)", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
