@@ -48,6 +48,9 @@ def parse():
                         "that scales rocprofv3's FETCH_SIZE / WRITE_SIZE readings")
     p.add_argument("--configs-only", action="store_true",
                    help="only time every BASELINE.json config (one JSON line)")
+    p.add_argument("--phase-timeline", action="store_true",
+                   help="only record the W8A8 ring kernel's per-workgroup tile phases on the two "
+                        "north-star GEMMs (needs the timeline build: make -C omni-rs_amd timeline)")
     return p.parse_args()
 
 
@@ -60,6 +63,76 @@ def copy_calibration():
         y.copy_(x)
     torch.cuda.synchronize()
     print(json.dumps({"copy_calibration_bytes": x.numel(), "copies": 3}))
+
+
+def phase_timeline(runs=24):
+    """Tile phases of the W8A8 ring kernel on the two north-star GEMMs
+    (try_int8_gemm, f32 out, operands rotated past the MALL as in the timed
+    bench), from the library built with OMNI_PHASE_TIMELINE: per unit (the
+    workgroup's 1st, 2nd, ... tile), medians over the workgroups of the K
+    loop's start (us from the first workgroup's start), its length and mean
+    shader clock, the next unit's copy issue, the epilogue, and the spread of
+    the epilogue's end (min / median / max), from the run of median length
+    among `runs` eager calls. One JSON line per shape."""
+    import ctypes
+    import numpy as np
+    here = os.path.dirname(os.path.abspath(__file__))
+    lib_path = os.path.join(here, "omni-rs_amd", "_timeline", "libomni_int8.so")
+    if not os.path.exists(lib_path):
+        raise SystemExit("no timeline build: run make -C omni-rs_amd timeline")
+    os.environ["OMNI_INT8_LIBRARY"] = lib_path
+    import torch
+    import omni_int8 as oi
+    lib = ctypes.CDLL(lib_path)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    for M, K, N in GEMM_SHAPES:
+        copies = max(4, -(-GEMV_ROTATION_BYTES // (2 * M * K + N * K + M * K)))
+        xs = [torch.randn((M, K), generator=gen, device=dev).half() for _ in range(copies)]
+        ws = [torch.randint(-127, 128, (N, K), generator=gen, device=dev, dtype=torch.int8)
+              for _ in range(copies)]
+        scale = torch.rand(N, generator=gen, device=dev) * 0.018 + 0.002
+        zero = torch.zeros(N, dtype=torch.int32, device=dev)
+        taken = []
+        for it in range(copies + runs):
+            k = it % copies
+            assert lib.omni_phase_timeline_clear() == 0
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            oi.try_int8_gemm(xs[k], ws[k].view(torch.int32).reshape(-1), scale, zero)
+            e1.record()
+            torch.cuda.synchronize()
+            if it >= copies:
+                buf = np.zeros(1024 * 64, dtype=np.uint64)
+                assert lib.omni_phase_timeline_read(buf.ctypes.data_as(ctypes.c_void_p),
+                                                    ctypes.c_size_t(buf.nbytes)) == 0
+                taken.append((e0.elapsed_time(e1) * 1e3, buf.reshape(1024, 64).astype(np.int64)))
+        taken.sort(key=lambda r: r[0])
+        op_us, ts = taken[len(taken) // 2]
+        ts = ts[ts[:, 62] > 0]                  # workgroups that ran
+        t0 = ts[:, 62].min()
+        units = []
+        for r in range(8):
+            done = ts[:, 8 * r + 3] > 0
+            if not done.any():
+                break
+            t = ts[done]
+            ks, ke, es, ee = ((t[:, 8 * r + c] - t0) / 100.0 for c in range(4))
+            mhz = (t[:, 8 * r + 5] - t[:, 8 * r + 4]) / np.maximum(ke - ks, 1e-3)
+            units.append({"unit": r, "workgroups": int(done.sum()),
+                          "k_start_us": round(float(np.median(ks)), 2),
+                          "k_loop_us": round(float(np.median(ke - ks)), 2),
+                          "k_loop_mhz": round(float(np.median(mhz))),
+                          "next_copies_us": round(float(np.median(es - ke)), 2),
+                          "epilogue_us": round(float(np.median(ee - es)), 2),
+                          "epilogue_end_us": [round(float(np.min(ee)), 2), round(float(np.median(ee)), 2),
+                                              round(float(np.max(ee)), 2)]})
+        print(json.dumps({"phase_timeline": {"M": M, "K": K, "N": N, "op_us": round(op_us, 1),
+                                             "kernel_span_us": units[-1]["epilogue_end_us"][2] if units else None,
+                                             "units": units}}), flush=True)
+        del xs, ws
 
 
 PROFILE_MARKS = []
@@ -706,6 +779,9 @@ def main():
     args = parse()
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.phase_timeline:
+        phase_timeline()
         return
     if args.configs_only:
         import torch

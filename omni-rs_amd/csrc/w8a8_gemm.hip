@@ -31,6 +31,27 @@
 
 namespace omni {
 
+#ifdef OMNI_PHASE_TIMELINE
+// Tile-phase timeline, in the library built with OMNI_PHASE_TIMELINE only
+// (make -C omni-rs_amd timeline; bench.py --phase-timeline reads it): thread
+// 0 of each ring-kernel workgroup b records, for its units r < 8, at
+// g_phase[b * 64 + 8 r + k] the 100 MHz real-time counter at the K loop's
+// start (k = 0, after the first barrier), the K loop's end (1), the
+// epilogue's start (2, after the next unit's first copies) and end (3), the
+// shader-clock counter at the K loop's start and end (4, 5), and at [b * 64 +
+// 62, 63] the real-time counter at the workgroup's start and its first unit
+// index. Vector stores from one lane, a few per unit.
+__device__ unsigned long long g_phase[1024 * 64];
+#define OMNI_PHASE(slot, value) \
+    do {                        \
+        if (phase && tid == 0) phase[(slot)] = (value); \
+    } while (0)
+#else
+#define OMNI_PHASE(slot, value) \
+    do {                        \
+    } while (0)
+#endif
+
 namespace {
 
 // crates/omni-kernel/src/int8_matmul.rs:156-158. Contraction is off so that
@@ -831,6 +852,12 @@ __global__ __launch_bounds__(64 * NW, 1) void w8a8_ring_kernel(W8A8Args a, int s
 
     int L = xcd_remap(blockIdx.x, gridDim.x);
     if (L >= units) return;
+#ifdef OMNI_PHASE_TIMELINE
+    unsigned long long* phase = blockIdx.x < 1024 ? g_phase + blockIdx.x * 64 : nullptr;
+    int unit_no = 0;
+#endif
+    OMNI_PHASE(62, __builtin_amdgcn_s_memrealtime());
+    OMNI_PHASE(63, (unsigned long long)L);
     if (tid == 0) sWide[0] = sWide[1] = sZero[0] = sZero[1] = 0;
     __syncthreads();
     tile_origin(L, m0, n0);
@@ -864,6 +891,11 @@ __global__ __launch_bounds__(64 * NW, 1) void w8a8_ring_kernel(W8A8Args a, int s
         // cleared for the tile after this one (store_params(parity ^ 1)
         // comes after this K loop's barriers).
         if (tid == 0) sWide[parity ^ 1] = sZero[parity ^ 1] = 0;
+#ifdef OMNI_PHASE_TIMELINE
+        if (unit_no >= 8) phase = nullptr;
+        OMNI_PHASE(8 * unit_no + 0, __builtin_amdgcn_s_memrealtime());
+        OMNI_PHASE(8 * unit_no + 4, __builtin_amdgcn_s_memtime());
+#endif
         read_frags(0, 0, fa0, fb0);
 
         if constexpr (PAIR) {
@@ -942,6 +974,10 @@ __global__ __launch_bounds__(64 * NW, 1) void w8a8_ring_kernel(W8A8Args a, int s
 
         const int64_t em0 = m0, en0 = n0;
         const int esplit = split;
+#ifdef OMNI_PHASE_TIMELINE
+        OMNI_PHASE(8 * unit_no + 1, __builtin_amdgcn_s_memrealtime());
+        OMNI_PHASE(8 * unit_no + 5, __builtin_amdgcn_s_memtime());
+#endif
         // Every wave is done reading the ring before the next tile's copies
         // (the clamped copies still in flight land first: one wave's loads
         // complete in issue order, and each wave writes its own LDS chunks).
@@ -955,6 +991,9 @@ __global__ __launch_bounds__(64 * NW, 1) void w8a8_ring_kernel(W8A8Args a, int s
             store_params(parity ^ 1);
             prologue();
         }
+#ifdef OMNI_PHASE_TIMELINE
+        OMNI_PHASE(8 * unit_no + 2, __builtin_amdgcn_s_memrealtime());
+#endif
 
         // Epilogue. 32x32 accumulator layout: lane holds column (lane & 31)
         // and rows 8*(r/4) + 4*(lane/32) + (r%4) of each 32x32 block.
@@ -1138,6 +1177,10 @@ __global__ __launch_bounds__(64 * NW, 1) void w8a8_ring_kernel(W8A8Args a, int s
         } else {
             full_epilogue(std::integral_constant<int, 2>{});
         }
+#ifdef OMNI_PHASE_TIMELINE
+        OMNI_PHASE(8 * unit_no + 3, __builtin_amdgcn_s_memrealtime());
+        ++unit_no;
+#endif
         if (!more) break;
         L = Ln;
         parity ^= 1;
@@ -1536,3 +1579,18 @@ hipError_t launch_w8a8_mfma(const W8A8Args& a, hipStream_t stream) {
 }
 
 }  // namespace omni
+
+#ifdef OMNI_PHASE_TIMELINE
+// Copies the tile-phase timeline (1024 workgroups x 64 entries) to dst;
+// returns a hipError_t code. Not part of the operator ABI.
+extern "C" int omni_phase_timeline_read(void* dst, size_t bytes) {
+    const size_t cap = sizeof(omni::g_phase);
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(omni::g_phase), bytes < cap ? bytes : cap, 0,
+                                    hipMemcpyDeviceToHost);
+}
+// Clears it (a synchronous copy of zeros; call outside any graph capture).
+extern "C" int omni_phase_timeline_clear() {
+    static unsigned long long zeros[1024 * 64];
+    return (int)hipMemcpyToSymbol(HIP_SYMBOL(omni::g_phase), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice);
+}
+#endif
