@@ -111,7 +111,8 @@ def phase_timeline(runs=24):
                 taken.append((e0.elapsed_time(e1) * 1e3, buf.reshape(1024, 64).astype(np.int64)))
         taken.sort(key=lambda r: r[0])
         op_us, ts = taken[len(taken) // 2]
-        ts = ts[ts[:, 62] > 0]                  # workgroups that ran
+        wg = np.nonzero(ts[:, 62] > 0)[0]       # workgroups that ran (index = blockIdx)
+        ts = ts[wg]
         t0 = ts[:, 62].min()
         units = []
         for r in range(8):
@@ -129,9 +130,15 @@ def phase_timeline(runs=24):
                           "epilogue_us": round(float(np.median(ee - es)), 2),
                           "epilogue_end_us": [round(float(np.min(ee)), 2), round(float(np.median(ee)), 2),
                                               round(float(np.max(ee)), 2)]})
+        # Each workgroup's last epilogue end, median over the workgroups of
+        # each XCD (dispatch places workgroup b on XCD b % 8).
+        last = np.max(np.where(ts[:, [8 * r + 3 for r in range(8)]] > 0,
+                               ts[:, [8 * r + 3 for r in range(8)]], 0), axis=1)
+        xcd_end = [round(float(np.median((last[wg % 8 == x] - t0) / 100.0)), 2) if (wg % 8 == x).any() else None
+                   for x in range(8)]
         print(json.dumps({"phase_timeline": {"M": M, "K": K, "N": N, "op_us": round(op_us, 1),
                                              "kernel_span_us": units[-1]["epilogue_end_us"][2] if units else None,
-                                             "units": units}}), flush=True)
+                                             "xcd_end_median_us": xcd_end, "units": units}}), flush=True)
         del xs, ws
 
 
