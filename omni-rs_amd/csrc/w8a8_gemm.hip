@@ -1033,6 +1033,10 @@ __global__ __launch_bounds__(64 * NW, 1) void w8a8_ring_kernel(W8A8Args a, int s
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
+#ifdef OMNI_PHASE_TIMELINE
+            OMNI_PHASE(8 * unit_no + 3, __builtin_amdgcn_s_memrealtime());
+            ++unit_no;
+#endif
             if (!more) break;
             L = Ln;
             parity ^= 1;
