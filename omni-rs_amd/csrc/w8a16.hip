@@ -328,8 +328,157 @@ __global__ __launch_bounds__(1024) void w8a16_gemv_kernel(W8A16Args a) {
     }
 }
 
+// Streamed decode GEMV for 2 to 4 activation rows, int8 weights, K == KF
+// (one 16-element chunk per lane, KF / 16 lanes rounded up to whole waves).
+// The weight rows come in batches of R; workgroup g takes batches g, g +
+// grid, ..., holding its lanes' x chunks of every row in registers for all
+// of them (x is read from L2 once per workgroup, not once per batch), with
+// the next batch's weights (and its output rows' scale and bias) in flight
+// while the current batch is summed: two register buffers, the loop
+// unrolled by two. Per batch: the same code conversion (1152 + w),
+// dot products, fold and cross-wave sum as w8a16_gemv_kernel, through a
+// parity-double-buffered LDS block, so one barrier per batch.
+template <int MR, int R, int KF>
+__global__ __launch_bounds__((KF / 16 + 63) / 64 * 64) void w8a16_gemv_stream_kernel(W8A16Args a) {
+    constexpr int kP = 8;                      // f16 pairs of x per chunk
+    constexpr int kChunks = KF / 16;
+    constexpr int kT = (kChunks + 63) / 64 * 64;
+    constexpr bool kExact = kT == kChunks;
+    constexpr int V = R * MR;
+    static_assert((V & (V - 1)) == 0 && V <= 64, "power-of-two partial count");
+    constexpr bool kBiased = R > MR;  // as in w8a16_gemv_kernel: more weight rows than x rows
+    static_assert(kT <= 1024, "one chunk per lane");
+    __shared__ float s_part[2][kT / 64][V];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int64_t K = KF;
+    const int64_t nb = (a.columns + R - 1) / R;
+    int64_t b = blockIdx.x;
+    if (b >= nb) return;  // the whole workgroup
+    const int64_t c = kExact || tid < kChunks ? tid : kChunks - 1;  // clamped chunks meet zero x
+    const bool live = kExact || tid < kChunks;
+
+    v2h xr[MR][kP];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        if (live && m < a.rows) {
+            const uint4* px = reinterpret_cast<const uint4*>(a.x + m * K + c * 16);
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const uint4 q = px[u];
+                xr[m][4 * u] = bits_half2(q.x);
+                xr[m][4 * u + 1] = bits_half2(q.y);
+                xr[m][4 * u + 2] = bits_half2(q.z);
+                xr[m][4 * u + 3] = bits_half2(q.w);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < kP; ++e) xr[m][e] = v2h{};
+        }
+    }
+    float xc[MR];
+    {
+        const v2h k1152 = {(_Float16)1152.0f, (_Float16)1152.0f};
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            xc[m] = 0.0f;
+            if constexpr (kBiased) {
+#pragma unroll
+                for (int e = 0; e < kP; ++e) xc[m] = __builtin_amdgcn_fdot2(k1152, xr[m][e], xc[m], false);
+            }
+        }
+    }
+
+    typedef unsigned v4u_t __attribute__((ext_vector_type(4)));
+    // Weights of batch bb, and (threads < V) scale and bias of the output
+    // row the thread writes.
+    auto load_batch = [&](int64_t bb, v4u_t (&w)[R], _Float16& sc, _Float16& bi) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int64_t n = bb * R + r < a.columns ? bb * R + r : a.columns - 1;
+            w[r] = __builtin_nontemporal_load(reinterpret_cast<const v4u_t*>(
+                reinterpret_cast<const uint8_t*>(a.w) + n * K + c * 16));
+        }
+        const int64_t ne = min(bb * R + (tid / MR) % R, a.columns - 1);
+        sc = a.scale[ne];
+        bi = (a.bias ? a.bias : a.scale)[ne];  // unconditional load
+    };
+    auto sum_batch = [&](int64_t bb, const v4u_t (&w)[R], _Float16 sc, _Float16 bi, int par) {
+        float part[V];
+#pragma unroll
+        for (int i = 0; i < V; ++i) part[i] = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const u32 words[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                v2h w01, w23;
+                if constexpr (kBiased)
+                    i8x4_to_f16x4_biased(words[q], w01, w23);
+                else
+                    i8x4_to_f16x4(words[q], w01, w23);
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    float& pp = part[r * MR + m];
+                    pp = __builtin_amdgcn_fdot2(w01, xr[m][2 * q], pp, false);
+                    pp = __builtin_amdgcn_fdot2(w23, xr[m][2 * q + 1], pp, false);
+                }
+            }
+        }
+        if constexpr (kBiased) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int m = 0; m < MR; ++m) part[r * MR + m] -= xc[m];
+        }
+        Fold<V, 32>::run(part, lane);
+        if ((lane & (64 / V - 1)) == 0) s_part[par][wave][fold_index<V>(lane)] = part[0];
+        __syncthreads();
+        if (tid < V) {
+            const int r = tid / MR, m = tid % MR;
+            const int64_t n = bb * R + r;
+            if (n < a.columns && m < a.rows) {
+                float acc = 0.0f;
+                for (int wv = 0; wv < kT / 64; ++wv) acc += s_part[par][wv][tid];
+                const float bias = a.bias ? (float)bi : 0.0f;
+                a.out[(int64_t)m * a.columns + n] = (_Float16)(acc * (float)sc + bias);
+            }
+        }
+    };
+
+    v4u_t wA[R], wB[R];
+    _Float16 scA, biA, scB, biB;
+    load_batch(b, wA, scA, biA);
+    while (true) {
+        const int64_t b1 = b + gridDim.x;
+        if (b1 < nb) load_batch(b1, wB, scB, biB);
+        sum_batch(b, wA, scA, biA, 0);
+        if (b1 >= nb) break;
+        const int64_t b2 = b1 + gridDim.x;
+        if (b2 < nb) load_batch(b2, wA, scA, biA);
+        sum_batch(b1, wB, scB, biB, 1);
+        if (b2 >= nb) break;
+        b = b2;
+    }
+}
+
+// Streamed GEMV launch: grid = min(batches, mult workgroups per CU).
+template <int MR, int R, int KF>
+hipError_t launch_gemv_stream(const W8A16Args& a, hipStream_t stream, int mult) {
+    if (a.width != KF) return hipErrorInvalidValue;
+    constexpr int kT = (KF / 16 + 63) / 64 * 64;
+    const int64_t nb = (a.columns + R - 1) / R;
+    const int64_t cap = (int64_t)num_cus() * mult;
+    const int64_t grid = nb < cap ? nb : cap;
+    hipLaunchKernelGGL((w8a16_gemv_stream_kernel<MR, R, KF>), dim3((unsigned)grid), dim3(kT), 0, stream, a);
+    return hipGetLastError();
+}
+
 // OMNI_W8A16_GEMV=<cpl><r> (e.g. 14 = one chunk per lane, four rows per
-// workgroup) pins the int8 GEMV configuration, OMNI_F16_GEMV the f16 one
+// workgroup; <1><r><b> with b batches per workgroup; 9<r><m> the streamed
+// GEMV, r = 4 or 8 rows a batch, m workgroups per CU, 2..4 rows at K = 4096
+// or 14336) pins the int8 GEMV configuration, OMNI_F16_GEMV the f16 one
 // (tuning knobs, omni::knob; unset = heuristic).
 int gemv_cfg_override(int wb) { return knob(wb == 8 ? Knob::W8A16Gemv : Knob::F16Gemv, 0); }
 
@@ -382,6 +531,20 @@ hipError_t launch_gemv_m(const W8A16Args& a, hipStream_t stream) {
         case 222: return launch_gemv_cfg<MR, 2, 2, WB, 2>(a, stream);
         default: break;
     }
+    if constexpr (WB == 8 && MR >= 2) {
+        // 9RM: the streamed GEMV with R = 4 (R digit 4) or 8 (8), M workgroups per CU.
+        const int ov = gemv_cfg_override(WB);
+        if (ov >= 900 && ov <= 999 && (a.width == 4096 || a.width == 14336)) {
+            const int rr = (ov / 10) % 10, mult = ov % 10;
+            if (mult >= 1 && (rr == 4 || rr == 8)) {
+                if (a.width == 4096)
+                    return rr == 8 ? launch_gemv_stream<MR, 8, 4096>(a, stream, mult)
+                                   : launch_gemv_stream<MR, 4, 4096>(a, stream, mult);
+                return rr == 8 ? launch_gemv_stream<MR, 8, 14336>(a, stream, mult)
+                               : launch_gemv_stream<MR, 4, 14336>(a, stream, mult);
+            }
+        }
+    }
     const int64_t chunks = a.width / (WB == 8 ? 16 : 8);
     if constexpr (WB == 16) {
         // f16 weights: 2048 chunks (K = 16384) fit one chunk each of 1024
@@ -401,6 +564,14 @@ hipError_t launch_gemv_m(const W8A16Args& a, hipStream_t stream) {
     // 4096 x 4096, 5 % at 4096 x 14336), batches of 8 beyond (the 128256-row
     // head, K = 14336).
     if (a.columns * a.width <= (4 << 20)) return launch_gemv_k<MR, 2, 1, WB>(a, stream);
+    // Two to four rows at K = 4096 on up to 32 M weights: the streamed GEMV,
+    // eight weight rows a batch, two workgroups per CU (MI355X, weights
+    // rotated past the MALL, 4096 x 4096: 5.54 against 5.90 us at M = 4, 5.02
+    // against 5.20 at M = 2; on the larger matrices its fewer workgroups keep
+    // less in flight and it is even or slower).
+    if constexpr (MR >= 2) {
+        if (a.width == 4096 && a.columns * a.width <= (32 << 20)) return launch_gemv_stream<MR, 8, 4096>(a, stream, 2);
+    }
     if (MR == 4 && chunks <= 512 && a.columns * a.width <= (64 << 20))
         return launch_gemv_cfg<MR, 1, 4, WB, 2>(a, stream);
     if (MR == 4 && chunks <= 1024) return launch_gemv_cfg<MR, 1, 8, WB, 2>(a, stream);

@@ -82,6 +82,34 @@ def test_gemv_every_configuration(oracle, monkeypatch, cfg, knobs):
         assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL, (cfg, rows, width, columns)
 
 
+@pytest.mark.parametrize("cfg", ["941", "942", "944", "981", "982", "984"])
+def test_gemv_stream_every_configuration(oracle, cfg, knobs):
+    # The streamed GEMV (OMNI_W8A16_GEMV=9<rows a batch><workgroups per CU>)
+    # on 2..4 activation rows at both K it is built for: ragged column counts
+    # (a last batch partly past the matrix), workgroups that take one batch
+    # or many, with and without a bias.
+    knobs.set("OMNI_W8A16_GEMV", cfg)
+    for rows, width, columns in ((2, 4096, 77), (3, 4096, 4099), (4, 4096, 9000), (2, 14336, 31),
+                                 (4, 14336, 4097), (3, 14336, 5)):
+        rng = np.random.default_rng(rows + width + columns + int(cfg))
+        x, w, s, b = make(rng, rows, width, columns, bias=columns % 2 == 1)
+        got = host(oi.w8a16_linear(dev(x), dev(w), dev(s), None if b is None else dev(b)))
+        ref = oracle.w8a16_f64(x, w, s, b)
+        assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL, (cfg, rows, width, columns)
+
+
+@pytest.mark.parametrize("rows", [2, 3, 4])
+@pytest.mark.parametrize("columns", [1025, 4096, 8191])
+def test_gemv_stream_default_route(oracle, rows, columns):
+    # 2..4 rows at K = 4096 on 4 M to 32 M weights take the streamed GEMV by
+    # default.
+    rng = np.random.default_rng(rows * 7 + columns)
+    x, w, s, b = make(rng, rows, 4096, columns, bias=True)
+    got = host(oi.w8a16_linear(dev(x), dev(w), dev(s), dev(b)))
+    ref = gpu_f64_reference(x, w, s, b)
+    assert tolerance.rel_err(got, ref) <= tolerance.FP16_REL_TOL, (rows, columns)
+
+
 @pytest.mark.parametrize("width,columns", [(4096, 4099), (14336, 4097), (1536, 8963), (8960, 1539),
                                           (1536, 515), (4096, 1027)])
 def test_gemv_k_builds_ragged_columns(oracle, width, columns):
