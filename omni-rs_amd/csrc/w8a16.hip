@@ -564,13 +564,14 @@ hipError_t launch_gemv_m(const W8A16Args& a, hipStream_t stream) {
     // 4096 x 4096, 5 % at 4096 x 14336), batches of 8 beyond (the 128256-row
     // head, K = 14336).
     if (a.columns * a.width <= (4 << 20)) return launch_gemv_k<MR, 2, 1, WB>(a, stream);
-    // Two to four rows at K = 4096 on up to 32 M weights: the streamed GEMV,
-    // eight weight rows a batch, two workgroups per CU (MI355X, weights
-    // rotated past the MALL, 4096 x 4096: 5.54 against 5.90 us at M = 4, 5.02
-    // against 5.20 at M = 2; on the larger matrices its fewer workgroups keep
-    // less in flight and it is even or slower).
+    // Two to four rows at K = 4096 on up to 64 M weights: the streamed GEMV
+    // with eight weight rows a batch and up to eight workgroups per CU, which
+    // at these sizes is one batch per workgroup (MI355X, weights rotated past
+    // the MALL: 4096 x 4096 5.54 against 5.90 us at M = 4, 5.02 against 5.20
+    // at M = 2; 4096 x 14336 13.0-13.3 against 13.2-14.1 at M = 4, 11.1
+    // against 11.6 at M = 2). On the 128256-row head it is 12 % slower.
     if constexpr (MR >= 2) {
-        if (a.width == 4096 && a.columns * a.width <= (32 << 20)) return launch_gemv_stream<MR, 8, 4096>(a, stream, 2);
+        if (a.width == 4096 && a.columns * a.width <= (64 << 20)) return launch_gemv_stream<MR, 8, 4096>(a, stream, 8);
     }
     if (MR == 4 && chunks <= 512 && a.columns * a.width <= (64 << 20))
         return launch_gemv_cfg<MR, 1, 4, WB, 2>(a, stream);

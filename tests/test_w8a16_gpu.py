@@ -99,9 +99,9 @@ def test_gemv_stream_every_configuration(oracle, cfg, knobs):
 
 
 @pytest.mark.parametrize("rows", [2, 3, 4])
-@pytest.mark.parametrize("columns", [1025, 4096, 8191])
+@pytest.mark.parametrize("columns", [1025, 4096, 8191, 14336, 16384])
 def test_gemv_stream_default_route(oracle, rows, columns):
-    # 2..4 rows at K = 4096 on 4 M to 32 M weights take the streamed GEMV by
+    # 2..4 rows at K = 4096 on 4 M to 64 M weights take the streamed GEMV by
     # default.
     rng = np.random.default_rng(rows * 7 + columns)
     x, w, s, b = make(rng, rows, 4096, columns, bias=True)
